@@ -1,0 +1,220 @@
+"""Headline benchmark: effective TOPS of the full `sageattn` call on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3c] [--no-cpu]
+
+A "step" is one full call (K/V prologue + main loop, Q quantized in the main loop) on synthetic
+inputs already resident in HBM. The default workload is BASELINE's headline, configs[2]: fp16,
+B=1, H=48, N=47520, D=128, causal, smooth_k on, HND. Ops convention 4*B*H*N^2*D, halved when
+causal (the reference's `bench/bench_attention.py:140`).
+
+Prints ONE JSON line. Besides the contract fields it carries
+* `roofline`: the main-loop kernel's achieved TFLOP/s (algorithmic ops per launch / its mean
+  launch duration, timed with HIP events on the launch stream inside the timed region) against
+  the int8/fp8 dense MFMA peak;
+* `prologue`: the prologue pair's achieved HBM GB/s on its algorithmic bytes;
+* `cpu_baseline`: the CPU emulation of the reference scheme (`oracle/`, a "port") and torch CPU
+  SDPA, timed on a bounded sample of the same workload on this host's cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "sageattention-rdna4_amd"))
+
+METRIC = "effective TOPS (full call incl. quant) fp16 B1 H48 D128 N47520 causal; % MFMA peak"
+PEAK_TOPS = 5000.0          # MI355X dense int8 (5.0 POPS) and fp8 (5.0 PFLOP/s) MFMA peak
+HBM_PEAK_GBPS = 8000.0
+
+WORKLOADS = {
+    # name: (dtype, B, H, N, causal, layout, k_offset_std, outlier_frac, std)
+    "c3c": ("fp16", 1, 48, 47520, True, "HND", 2.0, 0.0, 1.0),     # headline (configs[2], causal)
+    "c3n": ("fp16", 1, 48, 47520, False, "HND", 2.0, 0.0, 1.0),
+    "c2c": ("fp16", 1, 48, 8771, True, "HND", 2.0, 0.001, 1.0),
+    "c2n": ("fp16", 1, 48, 8771, False, "HND", 2.0, 0.001, 1.0),
+    "c4": ("bf16", 1, 48, 16384, True, "HND", 2.0, 0.001, 1.5),
+    "c1": ("fp16", 1, 48, 1024, False, "HND", 2.0, 0.0, 1.0),
+    "c5_288": ("fp16", 1, 48, 288, False, "HND", 0.0, 0.0, 1.0),
+    "c5_4096": ("fp16", 1, 48, 4096, False, "HND", 0.0, 0.0, 1.0),
+    "c5_b8": ("fp16", 8, 24, 4096, False, "NHD", 0.0, 0.0, 1.0),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_inputs(wl, seed=0):
+    import torch
+    dt, B, H, N, causal, layout, off, outl, std = wl
+    dtype = torch.float16 if dt == "fp16" else torch.bfloat16
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for i in range(3):
+        x = torch.randn(B, H, N, 128, generator=g, dtype=torch.float32)
+        if std != 1.0:
+            x.mul_(std)
+        if i == 1 and off:
+            x.add_(torch.randn(B, H, 1, 128, generator=g) * off)
+        if i == 1 and outl:
+            n_out = int(round(outl * N))
+            for b in range(B):
+                for h in range(H):
+                    idx = torch.randperm(N, generator=g)[:n_out]
+                    x[b, h, idx] *= 50.0
+        x = x.to(dtype)
+        if layout == "NHD":
+            x = x.transpose(1, 2).contiguous()
+        out.append(x)
+    return out
+
+
+def ops_of(B, H, N, causal):
+    return 4.0 * B * H * N * N * 128 * (0.5 if causal else 1.0)
+
+
+def prologue_bytes(B, H, N, smooth_k=True):
+    """Algorithmic HBM bytes of the prologue pair: K read twice (mean + quant) when smooth_k, V read
+    once, K8 and V8T written, SK and SV written, SV read and rewritten by the fold."""
+    n_pad = (N + 63) // 64 * 64
+    el = B * H * N * 128 * 2
+    q8 = B * H * n_pad * 128
+    return (2 if smooth_k else 1) * el + el + 2 * q8 + 4 * B * H * n_pad * 4
+
+
+def cpu_baseline(wl, q, k, v, budget_s=20.0):
+    """Time the oracle (CPU emulation of the reference scheme) and torch CPU SDPA on a bounded
+    sample of the workload: plane 0, the last `rows` query rows (the longest causal rows), with the
+    sample's prologue (mean, K/V quantization, fold) included."""
+    import torch
+    import torch.nn.functional as F
+    sys.path.insert(0, ROOT)
+    import oracle
+    dt, B, H, N, causal, layout, *_ = wl
+    qh, kh, vh = (oracle.to_hnd(t, layout)[0:1, 0:1].contiguous() for t in (q, k, v))
+    n_pad = oracle.n_pad_for(N)
+    sm = 128 ** -0.5
+    int8 = dt == "fp16"
+
+    def run(rows):
+        r0 = N - rows
+        t0 = time.perf_counter()
+        kr, vr, qr = kh[0], vh[0], qh[0]
+        mean = oracle.kseq_mean(kr)
+        k8, sk = oracle.quant_k(kr, n_pad, mean=mean, int8=int8)
+        v8t, sv = oracle.quant_v(vr, n_pad)
+        s, svp = oracle.fold_v_scale(sv)
+        q8, sq, cq = oracle.quant_q(qr[:, r0:], sm, int8=int8)
+        oracle.attention_tiles(q8, cq, k8, sk, v8t, svp, s, N, causal, q.dtype, row0=r0)
+        t_emu = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        qs = qr[:, r0:].float()
+        if causal:
+            mask = torch.arange(N)[None, :] <= torch.arange(r0, N)[:, None]
+            F.scaled_dot_product_attention(qs, kr.float(), vr.float(), attn_mask=mask)
+        else:
+            F.scaled_dot_product_attention(qs, kr.float(), vr.float())
+        t_sdpa = time.perf_counter() - t0
+        ops = sum(4.0 * 128 * ((r + 1) if causal else N) for r in range(r0, N))
+        return ops, t_emu, t_sdpa
+
+    rows = 64
+    ops, te, ts = run(rows)                      # warm-up and calibration
+    scale = max(1.0, budget_s / max(te + ts, 1e-3) * 0.8)
+    rows = int(min(N, max(64, rows * scale)) // 64 * 64) or 64
+    ops, te, ts = run(rows)
+    return dict(value=ops / te / 1e9, unit="GOPS", cores=torch.get_num_threads(), kind="port",
+                sample="plane 0 of %d, last %d query rows of N=%d%s, with that plane's prologue; "
+                       "ops %.3e, emulation %.2f s" % (B * H, rows, N, " (causal)" if causal else "",
+                                                       ops, te),
+                sdpa_cpu_gops=ops / ts / 1e9, sdpa_cpu_s=ts, host_cpus=os.cpu_count())
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c3c", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (every GPU box here has one GPU); "
+              "--gpus %d is not supported" % args.gpus, file=sys.stderr)
+        return 2
+
+    import torch
+    from sageattention import sageattn  # noqa: F401
+    from sageattention.sk1_backend import SageLib, sk1_forward
+
+    wl = WORKLOADS[args.workload]
+    dt, B, H, N, causal, layout, *_ = wl
+    q, k, v = make_inputs(wl)
+    dev = torch.device("cuda:0")
+    qd, kd, vd = (t.to(dev) for t in (q, k, v))
+    lib = SageLib.get()
+    call = lambda ev=None: sk1_forward(lib, qd, kd, vd, tensor_layout=layout, is_causal=causal,
+                                       smooth_k=True, events=ev)
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        call(evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    pro_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+    attn_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+    ev_ms = sum(e[0].elapsed_time(e[2]) for e in evs) / args.steps
+
+    ops = ops_of(B, H, N, causal)
+    value = ops / (ms_step * 1e-3) / 1e12
+    attn_tflops = ops / (attn_ms * 1e-3) / 1e12
+    pbytes = prologue_bytes(B, H, N)
+    pro_gbps = pbytes / (pro_ms * 1e-3) / 1e9
+    log("workload %s: %.3f ms/step (events %.3f), prologue %.3f ms (%.0f GB/s), main loop %.3f ms"
+        " (%.1f TFLOP/s)" % (args.workload, ms_step, ev_ms, pro_ms, pro_gbps, attn_ms, attn_tflops))
+
+    cpu = None
+    if not args.no_cpu:
+        del qd, kd, vd
+        cpu = cpu_baseline(wl, q, k, v, budget_s=args.cpu_budget)
+        log("cpu baseline:", cpu)
+
+    res = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8" if dt == "fp16" else "fp8",
+        "data": "synthetic",
+        "pct_mfma_peak": round(100.0 * value / PEAK_TOPS, 2),
+        "config": {"workload": "%s: %s B=%d H=%d N=%d D=128 %s smooth_k %s" % (
+            args.workload, dt, B, H, N, "causal" if causal else "non-causal", layout),
+            "global_batch": B, "seq_len": N, "parallelism": "single-gpu"},
+        "roofline": {"bound": "mfma", "achieved": round(attn_tflops, 1), "peak": PEAK_TOPS,
+                     "unit": "TFLOP/s", "frac": round(attn_tflops / PEAK_TOPS, 4),
+                     "traffic": None, "kernel": "attn_fwd_kernel", "ms": round(attn_ms, 4)},
+        "prologue": {"ms": round(pro_ms, 4), "bytes": pbytes, "achieved_GBps": round(pro_gbps, 1),
+                     "peak_GBps": HBM_PEAK_GBPS, "frac": round(pro_gbps / HBM_PEAK_GBPS, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,122 @@
+/*
+ * sage_mi355.h -- C ABI of the MI355X (gfx950) SageAttention SK1 library, libsagemi355.so.
+ *
+ * The library quantizes K and V per token (the "prologue") and runs the quantized flash-attention
+ * main loop (int8 Q.K on int8 MFMA for fp16 inputs, fp8 Q.K for bf16 inputs, fp8 P.V). It has no
+ * torch types: every tensor is a raw device pointer plus int64 element strides, every launch goes on
+ * the caller's HIP stream, the library never allocates device memory and never synchronizes the
+ * host. Every entry point returns SAGE_OK or a nonzero status; `sage_last_error()` gives the text.
+ *
+ * Layout vocabulary (the reference's, `sageattention/sk1_backend/sk1_loader.py:405-442`):
+ *   Q, K, V, O : logical (B, H, N, D=128) views, element strides (batch, head, row), last stride 1
+ *   N_pad      : ceil(N/64)*64
+ *   K8         : (B*H, N_pad, 128) int8 (qk_int8) or fp8 e4m3, row-major
+ *   SK, SV     : (B*H, N_pad) fp32 per-token scales
+ *   V8T        : (B*H, 128, N_pad) fp8 e4m3, V transposed
+ *   MEAN       : (B*H, 128) fp32 smooth_k mean
+ *   S          : (B*H) fp32 per-(b,h) V-scale fold
+ * dtype codes: SAGE_F16 = 0, SAGE_BF16 = 1.
+ */
+#ifndef SAGE_MI355_H
+#define SAGE_MI355_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SAGE_OK 0
+#define SAGE_ERR_INVALID 1 /* a contract violation: shape, stride, dtype, alignment, size */
+#define SAGE_ERR_HIP 2     /* a HIP runtime error (launch, device query) */
+
+#define SAGE_F16 0
+#define SAGE_BF16 1
+
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int sage_version(void);
+
+/* Text of the last error on the calling thread ("" if none). Valid until the next call. */
+const char* sage_last_error(void);
+
+/*
+ * Bytes of device workspace `sage_kv_prologue` needs for B*H planes of N rows.
+ * No reference counterpart: the reference allocates its mean with torch per call
+ * (`sageattention/sk1_backend/hip_prologue.py:219-222`).
+ */
+size_t sage_kv_prologue_workspace_bytes(int64_t BH, int64_t N);
+
+/*
+ * The K/V prologue: smooth_k mean, per-token K (int8 or fp8) and V (fp8) quantization, and the
+ * per-(b,h) V-scale fold, in two launches on `stream`.
+ *
+ * Replaces `HipPrologue.quant_kv` (`sageattention/sk1_backend/hip_prologue.py:188-244`), its
+ * kernels `h34_kseq_mean_{f16,bf16}` (`kernels/hip/h34_prologue.hip:284-294`) and
+ * `h34_quant_kv_{f16_i8,f16_f8,bf16_f8}` (`kernels/hip/h34_prologue.hip:214-242`), and
+ * `fold_v_scale` (`sageattention/sk1_backend/__init__.py:561-579`).
+ *
+ *   dtype     SAGE_F16 or SAGE_BF16 (K and V share it)
+ *   k_int8    1: K to int8 (fp16 only); 0: K to fp8 e4m3
+ *   smooth_k  1: subtract the sequence mean of K first
+ *   fold      1: write SV' = SV / S into `sv`; 0: leave SV unfolded (S is written either way)
+ *   k, v      logical (B, H, N, 128) views with element strides (k_sb, k_sh, k_sr) / (v_...)
+ *   outputs   k8, sk, v8t, sv, s (required); mean (may be NULL; written when smooth_k)
+ *   workspace at least sage_kv_prologue_workspace_bytes(B*H, N) bytes, 256-byte aligned
+ */
+int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int fold,
+                     const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sr,
+                     const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sr,
+                     int64_t B, int64_t H, int64_t N, int64_t N_pad,
+                     void* k8, float* sk, void* v8t, float* sv, float* mean, float* s,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The quantized flash-attention main loop (one launch on `stream`).
+ *
+ * Replaces `Sk1Attn.launch` / `Sk1Attn.launch_strided`
+ * (`sageattention/sk1_backend/sk1_loader.py:628-688`) and their kernels
+ * `sk1t6i_attn_fwd_c{0,1}` (`kernels/hip/sk1_t6i.hip:308-316`), `sk1t6in_attn_fwd_c{0,1}`
+ * (`kernels/hip/sk1_t6in.hip:323-332`) and `sk1t4a1{sb,nb}_attn_fwd_c{0,1}`
+ * (`kernels/hip/sk1_t4a1sb.hip:300-308`). Q is quantized per row inside the kernel (int8 when
+ * qk_int8, else fp8 e4m3); `sv` must hold SV' (the folded scales) and `s` the fold S.
+ *
+ *   q, o   logical (B, H, N, 128) views of `dtype`, element strides (q_sb, q_sh, q_sr) / (o_...)
+ *   k8 ... the prologue's outputs for the same B, H, N, N_pad and qk_int8
+ */
+int sage_attn_fwd(int dtype, int qk_int8, int causal,
+                  const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sr,
+                  const void* k8, const float* sk, const void* v8t, const float* sv,
+                  const float* s,
+                  void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr,
+                  int64_t B, int64_t H, int64_t N, int64_t N_pad, float sm_scale, void* stream);
+
+/*
+ * Q quantization exactly as the main loop performs it, written out for parity checks.
+ * Replaces the in-kernel Q quantization of `kernels/hip/sk1_t6i.hip:91-117` (int8) and
+ * `kernels/hip/sk1_t4a1s.hip:79-105` (fp8), which the reference never writes out.
+ *   q8  (B*H, N, 128) int8 or fp8; sq (B*H, N) fp32 = RN(amax/127) or RN(amax/448);
+ *   cq  (B*H, N) fp32 = RN(RN(sm_scale*log2e) * sq)
+ */
+int sage_quant_q(int dtype, int qk_int8,
+                 const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sr,
+                 int64_t B, int64_t H, int64_t N, float sm_scale,
+                 void* q8, float* sq, float* cq, void* stream);
+
+/*
+ * MFMA accumulator layout probe (known-answer test of the fragment layouts the main loop relies
+ * on). One wave computes C = A(32x32, int8) * B(32x32, int8) with v_mfma_i32_32x32x32_i8 and
+ * D = E(32x64, fp8) * F(64x32, fp8) with v_mfma_scale_f32_32x32x64_f8f6f4, loading operands in
+ * the main loop's fragment order and storing results by the assumed accumulator layout.
+ * Replaces `kernels/hip/sk1_layout_probe.hip:1-38` (the gfx1201 WMMA probe).
+ *   a (32x32 row-major int8, K contiguous), bt (32x32, B transposed: row n holds column n),
+ *   c (32x32 int32 out); e (32x64 fp8 row-major), ft (32x64 fp8, F transposed), d (32x32 fp32 out)
+ */
+int sage_mfma_layout_probe(const void* a, const void* bt, int32_t* c,
+                           const void* e, const void* ft, float* d, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAGE_MI355_H */

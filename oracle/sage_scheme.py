@@ -1,0 +1,271 @@
+"""The SK1 quantization scheme and attention loop, restated on the CPU in PyTorch fp32.
+
+TEST INFRASTRUCTURE ONLY (see the package docstring): the checker for the gfx950 kernels, never the
+product.
+
+Conventions:
+* RN(x) is one IEEE fp32 round-to-nearest-even operation. Every fp32 operation below is a single
+  torch CPU op on fp32 tensors, so each is one correctly rounded IEEE operation. No fused
+  multiply-add and no reassociation are used anywhere in the quantizers.
+* `torch.round` is round-half-to-even, the rule of `rintf` / `v_rndne_f32`.
+* `.to(torch.float8_e4m3fn)` is the OCP e4m3fn cast with round-to-nearest-even, the rule of the
+  hardware `v_cvt_pk_fp8_f32`. Every value cast here is already bounded by 448 in magnitude (up to
+  one fp32 rounding), so the cast's out-of-range behaviour is never reached.
+* Shapes are per (b, h) plane, flattened to `BH = B*H` in the leading axis: Q/K/V are (BH, N, D).
+
+Reference files (paths relative to the reference repository root):
+* `kernels/hip/h34_prologue.hip` -- the K/V prologue and the smooth_k mean;
+* `kernels/hip/sk1_t6i.hip` -- int8 Q.K main loop (fp16 inputs);
+* `kernels/hip/sk1_t4a1s.hip`, `kernels/hip/sk1_t4a1sb.hip` -- fp8 Q.K main loop (bf16 inputs);
+* `sageattention/sk1_backend/__init__.py` -- the per-(b,h) V-scale fold and the routing;
+* `sageattention/sk1_backend/hip_prologue.py` -- `n_pad_for`, the scale floor.
+"""
+import math
+
+import torch
+
+#: Key-tile width of the reference main loop and the padding granule of every quantized tensor
+#: (`kernels/hip/sk1_t6i.hip:24`, `sageattention/sk1_backend/hip_prologue.py:66`).
+BN = 64
+#: The int8/fp8 scale floor, fp32(1e-12) (`hip_prologue.py:188`, `h34_prologue.hip:147`).
+FLOOR = torch.tensor(1e-12, dtype=torch.float32)
+#: fp32(log2(e)) (`kernels/hip/sk1_t6i.hip:29`).
+LOG2E = torch.tensor(1.4426950408889634, dtype=torch.float32)
+#: e4m3 maximum and the P fold multiplier (`kernels/hip/sk1_t6i.hip:27`).
+P_SCALE = torch.tensor(448.0, dtype=torch.float32)
+#: int8 quantization range (`kernels/hip/sk1_t6i.hip:28`).
+I8_MAX = torch.tensor(127.0, dtype=torch.float32)
+
+F8 = torch.float8_e4m3fn
+
+
+def n_pad_for(N):
+    """`N_pad = ceil(N/64)*64` (`sageattention/sk1_backend/hip_prologue.py:93-95`)."""
+    return ((int(N) + BN - 1) // BN) * BN
+
+
+def to_hnd(x, tensor_layout):
+    """The logical (B, H, N, D) reading of a caller tensor (`sk1_backend/__init__.py:1035-1038`)."""
+    return x.transpose(1, 2) if tensor_layout == "NHD" else x
+
+
+def kseq_mean(k):
+    """smooth_k's sequence-axis mean (`kernels/hip/h34_prologue.hip:259-282`).
+
+    `mu[bh, d] = fp32( (sum_n fp64(k[bh, n, d])) / fp64(N) )`: every element is widened exactly to
+    fp64, summed in fp64, divided once in fp64 and rounded once to fp32. The fp64 sum is exact (so
+    independent of order) whenever every partial sum is representable, which holds for fp16 inputs
+    of magnitude below 2^10 at N < 2^19; the reference kernel's result is then the same bits.
+    `k`: (BH, N, D) fp16/bf16. Returns (BH, D) fp32.
+    """
+    N = k.shape[1]
+    s = k.to(torch.float64).sum(dim=1)
+    return (s / float(N)).to(torch.float32)
+
+
+def _pad_rows(x, n_pad):
+    BH, N, D = x.shape
+    out = torch.zeros(BH, n_pad, D, dtype=torch.float32)
+    out[:, :N] = x.to(torch.float32)
+    return out
+
+
+def quant_k(k, n_pad, mean=None, int8=True):
+    """K per-token quantization (`kernels/hip/h34_prologue.hip:116-165`).
+
+    * `kc = RN(fp32(k) - mu)` when a mean is given, else `fp32(k)`; pad rows (n >= N) are 0;
+    * `kmax = max_d |kc|`;
+    * int8 (fp16 inputs): `sk = max(RN(kmax / 127), FLOOR)`,
+      `K8 = clamp(rne(RN(kc / sk)), -128, 127)` -- a correctly rounded DIVISION
+      (`h34_prologue.hip:147`, `:156`, and the half-even rule of `:56-64`);
+    * fp8 (bf16 inputs): `sk = max(RN(kmax / 448), 1e-12)`, `K8 = e4m3(min(RN(kc / sk), 448))`,
+      no lower clamp (`h34_prologue.hip:158-165`);
+    * `SK = sk` on live rows and `1.0` on pad rows (`h34_prologue.hip:148`).
+
+    Returns `(K8 (BH, n_pad, D) int8 | float8_e4m3fn, SK (BH, n_pad) fp32)`.
+    """
+    BH, N, D = k.shape
+    kf = k.to(torch.float32)
+    if mean is not None:
+        kf = kf - mean[:, None, :].to(torch.float32)
+    kc = _pad_rows(kf, n_pad)
+    kmax = kc.abs().amax(dim=2)
+    if int8:
+        sk = torch.maximum(kmax / I8_MAX, FLOOR)
+        x = kc / sk[:, :, None]
+        k8 = torch.clamp(torch.round(x), -128.0, 127.0).to(torch.int8)
+    else:
+        sk = torch.maximum(kmax / P_SCALE, FLOOR)
+        x = torch.minimum(kc / sk[:, :, None], P_SCALE)
+        k8 = x.to(F8)
+    sk = sk.clone()
+    sk[:, N:] = 1.0
+    return k8, sk
+
+
+def quant_v(v, n_pad):
+    """V per-token fp8 quantization, stored transposed (`kernels/hip/h34_prologue.hip:168-211`).
+
+    `vmax = max_d |v|`; `sv = max(RN(vmax / 448), 1e-12)`; `SV = sv` on live rows, `0.0` on pad rows
+    (`h34_prologue.hip:186`); `V8T[d, n] = e4m3(min(RN(v[n, d] / sv), 448))`, 0 on pad rows.
+
+    Returns `(V8T (BH, D, n_pad) float8_e4m3fn, SV (BH, n_pad) fp32)`.
+    """
+    BH, N, D = v.shape
+    vf = _pad_rows(v, n_pad)
+    vmax = vf.abs().amax(dim=2)
+    sv = torch.maximum(vmax / P_SCALE, FLOOR)
+    x = torch.minimum(vf / sv[:, :, None], P_SCALE)
+    v8t = x.to(F8).transpose(1, 2).contiguous()
+    sv = sv.clone()
+    sv[:, N:] = 0.0
+    return v8t, sv
+
+
+def fold_v_scale(sv):
+    """The per-(b,h) V-scale fold (`sageattention/sk1_backend/__init__.py:561-579`).
+
+    `S = max(max_n SV[n], 1.0)` and `SV' = RN(SV / S)`. `S == 1` exactly when every `|v| <= 448`,
+    and then `SV'` is `SV` bit for bit. Returns `(S (BH,) fp32, SV' (BH, n_pad) fp32)`.
+    """
+    s = torch.clamp_min(sv.amax(dim=1), 1.0)
+    return s, sv / s[:, None]
+
+
+def quant_q(q, sm_scale, int8=True):
+    """Per-query-row Q quantization done inside the reference main loop.
+
+    int8 (`kernels/hip/sk1_t6i.hip:91-117`): `amax = max(max_d |q|, 1e-12)`; `qinv = RN(127 / amax)`;
+    `Q8 = clamp(rne(RN(q * qinv)), -128, 127)` -- multiplication by a correctly rounded
+    RECIPROCAL, unlike K's division; `sq = RN(amax / 127)`; `c_q = RN(RN(sm * LOG2E) * sq)`.
+
+    fp8 (`kernels/hip/sk1_t4a1s.hip:79-105`, templated by `sk1_t4a1sb.hip`):
+    `qinv = RN(448 / amax)`; `Q8 = e4m3(clamp(RN(q * qinv), -448, 448))`; `sq = RN(amax / 448)`.
+
+    `q`: (BH, N, D) fp16/bf16. Returns `(Q8 (BH, N, D), sq (BH, N) fp32, c_q (BH, N) fp32)`.
+    """
+    qf = q.to(torch.float32)
+    amax = torch.maximum(qf.abs().amax(dim=2), FLOOR)
+    sm = torch.tensor(float(sm_scale), dtype=torch.float32)
+    top = I8_MAX if int8 else P_SCALE
+    qinv = top / amax
+    x = qf * qinv[:, :, None]
+    if int8:
+        q8 = torch.clamp(torch.round(x), -128.0, 127.0).to(torch.int8)
+    else:
+        q8 = torch.clamp(x, -P_SCALE, P_SCALE).to(F8)
+    sq = amax / top
+    c_q = (sm * LOG2E) * sq
+    return q8, sq, c_q
+
+
+def attention_tiles(q8, c_q, k8, sk, v8t, svp, s_fold, N, causal, out_dtype, tile=BN,
+                    q_chunk=2048, row0=0):
+    """The main loop's online softmax over key tiles, in the reference's phase order.
+
+    Follows `kernels/hip/sk1_t6i.hip:162-299` (and the identical fp8 form of `sk1_t4a1s.hip`):
+    per key tile of `tile` keys, in order,
+    * `s = RN(fp32(sum_d Q8*K8) * RN(c_q * SK[n]))` (the int8 dot product is exact in fp32:
+      |sum| <= 128^3 = 2^21 < 2^24); masked keys (causal `n > m`; non-causal `n >= N`) are -inf;
+    * `m_new = max(m, max_tile s)`; `m_use = m_new`, or 0 when it is -inf; `alpha = exp2(m - m_use)`;
+    * `p = exp2(s - m_use)`; `l = l*alpha + sum_tile p` (the row sum is taken before the fold);
+    * `p8 = e4m3(RN(p * RN(SV'[n] * 448)))`; `acc = acc*alpha + sum_n p8 * V8[n]` in fp32;
+    and the epilogue `O = T(acc * (l > 0 ? RN(S / RN(l * 448)) : 0))` (`sk1_t6i.hip:281-299`).
+
+    The GPU uses the hardware `exp2` and an unspecified MFMA accumulation order, so the output is
+    pinned by tolerance, not bits. Queries are processed in chunks of `q_chunk` rows to bound
+    memory; chunking queries does not change any per-row arithmetic. `row0` is the sequence index of
+    the first row of `q8` (for computing a subset of rows: rows are independent).
+
+    Shapes: q8 (BH, N, D); c_q (BH, N); k8 (BH, n_pad, D); sk, svp (BH, n_pad); v8t (BH, D, n_pad);
+    s_fold (BH,). Returns O (BH, N, D) in `out_dtype`.
+    """
+    BH, NQ, D = q8.shape
+    n_pad = k8.shape[1]
+    kf = k8.to(torch.float32)
+    vf = v8t.to(torch.float32)
+    sv448 = svp * P_SCALE
+    out = torch.empty(BH, NQ, D, dtype=out_dtype)
+    neg_inf = torch.tensor(-math.inf, dtype=torch.float32)
+    for r0 in range(0, NQ, q_chunk):
+        r1 = min(NQ, r0 + q_chunk)
+        qf = q8[:, r0:r1].to(torch.float32)
+        cq = c_q[:, r0:r1]
+        rows = torch.arange(row0 + r0, row0 + r1)[:, None]
+        m = torch.full((BH, r1 - r0), -math.inf, dtype=torch.float32)
+        l = torch.zeros(BH, r1 - r0, dtype=torch.float32)
+        acc = torch.zeros(BH, r1 - r0, D, dtype=torch.float32)
+        n_tiles = n_pad // tile
+        if causal:
+            n_tiles = min(n_tiles, (row0 + r1 - 1) // tile + 1)
+        for j in range(n_tiles):
+            ks = slice(j * tile, (j + 1) * tile)
+            dot = torch.matmul(qf, kf[:, ks].transpose(1, 2))
+            s = dot * (cq[:, :, None] * sk[:, None, ks])
+            keys = torch.arange(j * tile, (j + 1) * tile)[None, :]
+            dead = (keys > rows) if causal else (keys >= N)
+            s = torch.where(dead[None], neg_inf, s)
+            m_new = torch.maximum(m, s.amax(dim=2))
+            m_use = torch.where(m_new == -math.inf, torch.zeros_like(m_new), m_new)
+            alpha = torch.exp2(m - m_use)
+            p = torch.exp2(s - m_use[:, :, None])
+            l = l * alpha + p.sum(dim=2)
+            p8 = (p * sv448[:, None, ks]).to(F8).to(torch.float32)
+            acc = acc * alpha[:, :, None] + torch.matmul(p8, vf[:, :, ks].transpose(1, 2))
+            m = m_new
+        inv = torch.where(l > 0, s_fold[:, None] / (l * P_SCALE), torch.zeros_like(l))
+        out[:, r0:r1] = (acc * inv[:, :, None]).to(out_dtype)
+    return out
+
+
+def emulate_sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=None, smooth_k=True,
+                     qk_int8=None):
+    """The whole SK1 call on the CPU, returning every intermediate.
+
+    Routing follows `sageattention/sk1_backend/__init__.py:1161-1272`: fp16 inputs use int8 Q.K
+    (`sk1_t6i`), bf16 inputs use fp8 Q.K (`sk1_t4a1sb`); `qk_int8=False` forces the fp8 form for
+    fp16 inputs. `sm_scale` defaults to `D ** -0.5` (`__init__.py:1165`).
+
+    Returns a dict with `mean, k8, sk, v8t, sv, s, svp, q8, sq, c_q, o` where `o` has the caller's
+    layout and dtype and every other tensor is per (b, h) plane, (BH, ...).
+    """
+    qq, kk, vv = (to_hnd(t, tensor_layout) for t in (q, k, v))
+    B, H, N, D = qq.shape
+    BH = B * H
+    if qk_int8 is None:
+        qk_int8 = (q.dtype == torch.float16)
+    sm = float(sm_scale if sm_scale is not None else D ** -0.5)
+    n_pad = n_pad_for(N)
+    qr, kr, vr = (t.reshape(BH, N, D) for t in (qq, kk, vv))
+    mean = kseq_mean(kr) if smooth_k else None
+    k8, sk = quant_k(kr, n_pad, mean=mean, int8=qk_int8)
+    v8t, sv = quant_v(vr, n_pad)
+    s, svp = fold_v_scale(sv)
+    q8, sq, c_q = quant_q(qr, sm, int8=qk_int8)
+    o = attention_tiles(q8, c_q, k8, sk, v8t, svp, s, N, is_causal, q.dtype)
+    o = o.view(B, H, N, D)
+    if tensor_layout == "NHD":
+        o = o.transpose(1, 2).contiguous()
+    return dict(mean=mean, k8=k8, sk=sk, v8t=v8t, sv=sv, s=s, svp=svp, q8=q8, sq=sq, c_q=c_q, o=o,
+                n_pad=n_pad, sm_scale=sm)
+
+
+def exact_attention(q, k, v, is_causal=False, sm_scale=None, tensor_layout="HND", q_chunk=1024):
+    """Unquantized attention in fp64, chunked over queries (the error yardstick, not the oracle).
+
+    Returns fp64 output in the caller's layout.
+    """
+    qq, kk, vv = (to_hnd(t, tensor_layout).to(torch.float64) for t in (q, k, v))
+    B, H, N, D = qq.shape
+    sm = float(sm_scale if sm_scale is not None else D ** -0.5)
+    out = torch.empty(B, H, N, D, dtype=torch.float64)
+    for r0 in range(0, N, q_chunk):
+        r1 = min(N, r0 + q_chunk)
+        s = torch.matmul(qq[:, :, r0:r1], kk.transpose(2, 3)) * sm
+        if is_causal:
+            dead = torch.arange(N)[None, :] > torch.arange(r0, r1)[:, None]
+            s = s.masked_fill(dead, -math.inf)
+        out[:, :, r0:r1] = torch.matmul(torch.softmax(s, dim=-1), vv)
+    if tensor_layout == "NHD":
+        out = out.transpose(1, 2)
+    return out

@@ -1,0 +1,67 @@
+"""Build libsagemi355.so, the gfx950 HIP library behind `sageattention`, in-tree.
+
+    python sageattention-rdna4_amd/build_lib.py [--verbose]
+
+Compiles every `csrc/*.hip` for `--offload-arch=gfx950` with hipcc (in parallel, one process per
+translation unit) and links them into `sageattention/_lib/libsagemi355.so`. Flags that matter for
+numerics: no fast-math (fp32 division stays correctly rounded), and packed-fp32 code generation
+disabled (`-Xclang -target-feature -Xclang -packed-fp32-ops`).
+"""
+import concurrent.futures
+import glob
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIB_DIR = os.path.join(HERE, "sageattention", "_lib")
+LIB_NAME = "libsagemi355.so"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+COMMON_FLAGS = [
+    "--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-command-line-argument",
+]
+
+
+def lib_path():
+    return os.path.join(LIB_DIR, LIB_NAME)
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature: harmless, not shown.
+    noise = ("packed-fp32-ops", "is not a recognized feature for this target")
+    err = "\n".join(l for l in res.stderr.splitlines() if not any(n in l for n in noise))
+    if res.returncode != 0:
+        raise RuntimeError("command failed (%d): %s\n%s" % (res.returncode, " ".join(cmd), err))
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+    return res
+
+
+def build(verbose=False, jobs=None):
+    """Compile and link the library; returns its path. Always rebuilds."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    obj_dir = os.path.join(HERE, "_build")
+    os.makedirs(obj_dir, exist_ok=True)
+    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    if not sources:
+        raise RuntimeError("no HIP sources under %s" % CSRC)
+    objs = [os.path.join(obj_dir, os.path.splitext(os.path.basename(s))[0] + ".o") for s in sources]
+    cmds = [[HIPCC] + COMMON_FLAGS + ["-c", s, "-o", o] for s, o in zip(sources, objs)]
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs or min(8, len(cmds))) as ex:
+        list(ex.map(lambda c: _run(c, verbose), cmds))
+    out = lib_path()
+    tmp = out + ".tmp"
+    _run([HIPCC, "--offload-arch=" + ARCH, "-shared", "-fPIC", "-o", tmp] + objs, verbose)
+    os.replace(tmp, out)
+    return out
+
+
+if __name__ == "__main__":
+    print(build(verbose="--verbose" in sys.argv))

@@ -1,0 +1,202 @@
+// The C ABI of libsagemi355.so (declared in include/sage_mi355.h): argument contracts, error
+// reporting, and the calls into the kernel launchers. Nothing here allocates device memory or
+// synchronizes the host.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/sage_mi355.h"
+#include "sage_launch.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) {
+    g_err.clear();
+    return SAGE_OK;
+  }
+  return fail(SAGE_ERR_HIP, "%s: %s (%s)", what, hipGetErrorName(e), hipGetErrorString(e));
+}
+
+constexpr int64_t kInt32Max = 2147483647LL;
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// The stride rule of the 16-byte vector accesses (the reference's `strided_view_reason`,
+// sageattention/sk1_backend/sk1_loader.py:313-369): positive, multiples of 8 elements.
+int check_view(const char* name, const void* p, int64_t sb, int64_t sh, int64_t sr) {
+  if (p == nullptr) return fail(SAGE_ERR_INVALID, "%s is NULL", name);
+  if (!aligned16(p)) return fail(SAGE_ERR_INVALID, "%s: ptr_align (pointer not 16-byte aligned)", name);
+  if (sb <= 0 || sh <= 0 || sr <= 0)
+    return fail(SAGE_ERR_INVALID, "%s: stride_nonpos (%lld, %lld, %lld)", name, (long long)sb,
+                (long long)sh, (long long)sr);
+  if ((sb | sh | sr) & 7)
+    return fail(SAGE_ERR_INVALID, "%s: stride_align (strides must be multiples of 8 elements)", name);
+  return SAGE_OK;
+}
+
+int check_shape(int64_t B, int64_t H, int64_t N, int64_t N_pad) {
+  if (B < 1 || H < 1) return fail(SAGE_ERR_INVALID, "B and H must be >= 1 (B=%lld H=%lld)",
+                                  (long long)B, (long long)H);
+  if (N < 1) return fail(SAGE_ERR_INVALID, "n_lt_1: N must be >= 1 (N=%lld)", (long long)N);
+  if (N_pad < N || (N_pad % 64) != 0)
+    return fail(SAGE_ERR_INVALID, "n_pad: N_pad must be a multiple of 64 and >= N (N=%lld N_pad=%lld)",
+                (long long)N, (long long)N_pad);
+  if (B * H > 65535 || N_pad > kInt32Max / 128 || B * H * ((N + 127) / 128) > kInt32Max)
+    return fail(SAGE_ERR_INVALID, "shape too large for the grid (B*H=%lld N=%lld)",
+                (long long)(B * H), (long long)N);
+  return SAGE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sage_version(void) { return 100; }
+
+const char* sage_last_error(void) { return g_err.c_str(); }
+
+size_t sage_kv_prologue_workspace_bytes(int64_t BH, int64_t N) {
+  if (BH < 1 || N < 1) return 0;
+  return sage::prologue_workspace_bytes(BH, (N + 63) / 64 * 64);
+}
+
+int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int fold, const void* k, int64_t k_sb,
+                     int64_t k_sh, int64_t k_sr, const void* v, int64_t v_sb, int64_t v_sh,
+                     int64_t v_sr, int64_t B, int64_t H, int64_t N, int64_t N_pad, void* k8,
+                     float* sk, void* v8t, float* sv, float* mean, float* s, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  if (dtype != SAGE_F16 && dtype != SAGE_BF16)
+    return fail(SAGE_ERR_INVALID, "dtype: unsupported dtype code %d", dtype);
+  if (dtype == SAGE_BF16 && k_int8)
+    return fail(SAGE_ERR_INVALID, "bf16_int8: int8 K is served for fp16 inputs only");
+  int rc = check_shape(B, H, N, N_pad);
+  if (rc) return rc;
+  if ((rc = check_view("k", k, k_sb, k_sh, k_sr))) return rc;
+  if ((rc = check_view("v", v, v_sb, v_sh, v_sr))) return rc;
+  if (!k8 || !sk || !v8t || !sv || !s) return fail(SAGE_ERR_INVALID, "an output pointer is NULL");
+  if (!aligned16(k8) || !aligned16(v8t) || !aligned16(sk) || !aligned16(sv))
+    return fail(SAGE_ERR_INVALID, "ptr_align: outputs must be 16-byte aligned");
+  const size_t need = sage::prologue_workspace_bytes(B * H, N_pad);
+  if (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 255u))
+    return fail(SAGE_ERR_INVALID, "workspace: need %zu bytes, 256-byte aligned (got %zu)", need,
+                workspace_bytes);
+  sage::PrologueArgs a;
+  a.dtype = dtype;
+  a.k_int8 = k_int8 ? 1 : 0;
+  a.smooth_k = smooth_k ? 1 : 0;
+  a.fold = fold ? 1 : 0;
+  a.k = k;
+  a.k_sb = k_sb;
+  a.k_sh = k_sh;
+  a.k_sr = k_sr;
+  a.v = v;
+  a.v_sb = v_sb;
+  a.v_sh = v_sh;
+  a.v_sr = v_sr;
+  a.B = B;
+  a.H = H;
+  a.N = N;
+  a.N_pad = N_pad;
+  a.k8 = k8;
+  a.sk = sk;
+  a.v8t = v8t;
+  a.sv = sv;
+  a.mean = smooth_k ? mean : nullptr;
+  a.s = s;
+  a.workspace = workspace;
+  return hip_status(sage::launch_prologue(a, (hipStream_t)stream), "sage_kv_prologue launch");
+}
+
+int sage_attn_fwd(int dtype, int qk_int8, int causal, const void* q, int64_t q_sb, int64_t q_sh,
+                  int64_t q_sr, const void* k8, const float* sk, const void* v8t, const float* sv,
+                  const float* s, void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr, int64_t B,
+                  int64_t H, int64_t N, int64_t N_pad, float sm_scale, void* stream) {
+  if (dtype != SAGE_F16 && dtype != SAGE_BF16)
+    return fail(SAGE_ERR_INVALID, "dtype: unsupported dtype code %d", dtype);
+  if (dtype == SAGE_BF16 && qk_int8)
+    return fail(SAGE_ERR_INVALID, "bf16_int8: int8 Q.K is served for fp16 inputs only");
+  int rc = check_shape(B, H, N, N_pad);
+  if (rc) return rc;
+  if ((rc = check_view("q", q, q_sb, q_sh, q_sr))) return rc;
+  if ((rc = check_view("o", o, o_sb, o_sh, o_sr))) return rc;
+  if (!k8 || !sk || !v8t || !sv || !s) return fail(SAGE_ERR_INVALID, "an input pointer is NULL");
+  if (!aligned16(k8) || !aligned16(v8t) || !aligned16(sk) || !aligned16(sv))
+    return fail(SAGE_ERR_INVALID, "ptr_align: quantized inputs must be 16-byte aligned");
+  sage::AttnArgs a;
+  a.dtype = dtype;
+  a.qk_int8 = qk_int8 ? 1 : 0;
+  a.causal = causal ? 1 : 0;
+  a.q = q;
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.q_sr = q_sr;
+  a.k8 = k8;
+  a.sk = sk;
+  a.v8t = v8t;
+  a.sv = sv;
+  a.s = s;
+  a.o = o;
+  a.o_sb = o_sb;
+  a.o_sh = o_sh;
+  a.o_sr = o_sr;
+  a.B = B;
+  a.H = H;
+  a.N = N;
+  a.N_pad = N_pad;
+  a.sm_scale = sm_scale;
+  return hip_status(sage::launch_attn_fwd(a, (hipStream_t)stream), "sage_attn_fwd launch");
+}
+
+int sage_quant_q(int dtype, int qk_int8, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sr,
+                 int64_t B, int64_t H, int64_t N, float sm_scale, void* q8, float* sq, float* cq,
+                 void* stream) {
+  if (dtype != SAGE_F16 && dtype != SAGE_BF16)
+    return fail(SAGE_ERR_INVALID, "dtype: unsupported dtype code %d", dtype);
+  if (dtype == SAGE_BF16 && qk_int8)
+    return fail(SAGE_ERR_INVALID, "bf16_int8: int8 Q is served for fp16 inputs only");
+  int rc = check_shape(B, H, N, (N + 63) / 64 * 64);
+  if (rc) return rc;
+  if ((rc = check_view("q", q, q_sb, q_sh, q_sr))) return rc;
+  if (!q8 || !sq || !cq) return fail(SAGE_ERR_INVALID, "an output pointer is NULL");
+  if (!aligned16(q8)) return fail(SAGE_ERR_INVALID, "ptr_align: q8 must be 16-byte aligned");
+  sage::QuantQArgs a;
+  a.dtype = dtype;
+  a.qk_int8 = qk_int8 ? 1 : 0;
+  a.q = q;
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.q_sr = q_sr;
+  a.B = B;
+  a.H = H;
+  a.N = N;
+  a.sm_scale = sm_scale;
+  a.q8 = q8;
+  a.sq = sq;
+  a.cq = cq;
+  return hip_status(sage::launch_quant_q(a, (hipStream_t)stream), "sage_quant_q launch");
+}
+
+int sage_mfma_layout_probe(const void* a, const void* bt, int32_t* c, const void* e,
+                           const void* ft, float* d, void* stream) {
+  if (!a || !bt || !c || !e || !ft || !d) return fail(SAGE_ERR_INVALID, "a pointer is NULL");
+  if (!aligned16(a) || !aligned16(bt) || !aligned16(e) || !aligned16(ft))
+    return fail(SAGE_ERR_INVALID, "ptr_align: operands must be 16-byte aligned");
+  return hip_status(sage::launch_layout_probe(a, bt, c, e, ft, d, (hipStream_t)stream),
+                    "sage_mfma_layout_probe launch");
+}
+
+}  // extern "C"

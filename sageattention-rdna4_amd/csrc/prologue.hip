@@ -1,0 +1,287 @@
+// The K/V prologue on gfx950: two launches, both HBM-bound streaming passes.
+//
+//   1. stats pass  (kv_stats_kernel):  reads K and V once.
+//        * K: per-column fp64 partial sums over the block's rows (the smooth_k mean), written to the
+//          workspace as C1 partials per plane -- no atomics, so the sum order is fixed;
+//        * V: per-token scale sv = max(RN(vmax/448), 1e-12), e4m3 quantization, and the transposed
+//          store V8T[d][n] through an LDS tile; SV is written; the block's max sv goes to the
+//          workspace for the fold.
+//   2. quant pass  (k_quant_kernel):   reads K again.
+//        * reduces the C1 mean partials of its plane in a fixed order (every block gets the same
+//          bits), mu = fp32(sum / N);
+//        * S = max(1, max sv) from the stats partials; SV' = RN(SV / S) in place for its rows;
+//        * K per-token quantization: int8 (round half to even, clamp) or e4m3.
+//
+// The arithmetic restates kernels/hip/h34_prologue.hip:116-211 (K and V quantizers),
+// :259-282 (fp64 mean) and sageattention/sk1_backend/__init__.py:561-579 (the S fold) of the
+// reference. The mean is fp64-accumulated from exactly widened inputs like the reference's; the
+// summation order differs, which cannot change the bits whenever the fp64 sum is exact (fp16 data
+// of magnitude below 2^10 at N below 2^19 -- every served shape of interest).
+//
+// Thread layout of both passes: 256 threads = 16 column groups (cg, 8 columns = one 16-byte load)
+// x 16 row groups (rg). The 16 lanes sharing a row are one aligned 16-lane group of a wave, so a
+// row's absmax is a 4-step xor shuffle.
+#include "sage_device.h"
+#include "sage_launch.h"
+
+namespace sage {
+
+constexpr int PT = 256;          // threads per block
+constexpr int STEP = 128;        // rows per stats step (one V8T tile)
+constexpr int VT_STRIDE = 144;   // LDS bytes per transposed-V row (128 tokens + 16 pad)
+
+PrologueGeom prologue_geom(int64_t BH, int64_t N_pad) {
+  auto clampr = [](int64_t x, int64_t lo, int64_t hi) { return x < lo ? lo : (x > hi ? hi : x); };
+  auto up128 = [](int64_t x) { return (x + 127) / 128 * 128; };
+  PrologueGeom g;
+  // Aim for ~1024 stats blocks and ~2048 quant blocks on big calls.
+  g.R1 = clampr(up128((N_pad * BH + 1023) / 1024), 128, 2048);
+  g.C1 = (N_pad + g.R1 - 1) / g.R1;
+  g.R2 = clampr(up128((N_pad * BH + 2047) / 2048), 128, 1024);
+  g.C2 = (N_pad + g.R2 - 1) / g.R2;
+  return g;
+}
+
+size_t prologue_workspace_bytes(int64_t BH, int64_t N_pad) {
+  const PrologueGeom g = prologue_geom(BH, N_pad);
+  const size_t part = (size_t)BH * g.C1 * HD * sizeof(double);
+  const size_t smax = (size_t)BH * g.C1 * sizeof(float);
+  return ((part + 255) / 256 * 256) + ((smax + 255) / 256 * 256);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Stats pass. grid (C1, BH), block 256.
+// In a 128-row step, thread (cg, rg) owns rows 8rg .. 8rg+7 and columns 8cg .. 8cg+7, so for each
+// of its 8 columns it holds 8 consecutive tokens: one 8-byte word of the transposed tile. The LDS
+// tile is [128 d][144 B]; the 8-byte chunk of tokens 8rg..8rg+7 of row d sits at chunk position
+// rg ^ (d >> 3), which keeps both the column writes and the row reads free of bank conflicts.
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(PT) void kv_stats_kernel(
+    const T* __restrict__ K, const T* __restrict__ V, u8* __restrict__ V8T, float* __restrict__ SV,
+    double* __restrict__ part, float* __restrict__ smax, int64_t H, int64_t N, int64_t N_pad,
+    int64_t R1, int64_t C1, int64_t k_sb, int64_t k_sh, int64_t k_sr, int64_t v_sb, int64_t v_sh,
+    int64_t v_sr, int smooth_k) {
+  __shared__ __attribute__((aligned(16))) u8 tile[HD * VT_STRIDE];
+  __shared__ float wmax[PT / 64];
+
+  const int tid = threadIdx.x, cg = tid & 15, rg = tid >> 4;
+  const int64_t c = blockIdx.x, bh = blockIdx.y;
+  const int64_t b = bh / H, h = bh - b * H;
+  const T* kp = K + b * k_sb + h * k_sh + 8 * cg;
+  const T* vp = V + b * v_sb + h * v_sh + 8 * cg;
+  u8* vt = V8T + bh * HD * N_pad;
+  const int64_t r_begin = c * R1;
+  const int64_t r_end = (r_begin + R1 < N_pad) ? r_begin + R1 : N_pad;
+
+  double ks[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ks[i] = 0.0;
+  float sv_max = 0.0f;
+
+  for (int64_t n0 = r_begin; n0 < r_end; n0 += STEP) {
+    u32x4 vw[8], kw[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t n = n0 + 8 * rg + i;
+      const bool live = n < N;
+      vw[i] = live ? *(const u32x4*)(vp + n * v_sr) : (u32x4){0u, 0u, 0u, 0u};
+      kw[i] = (live && smooth_k) ? *(const u32x4*)(kp + n * k_sr) : (u32x4){0u, 0u, 0u, 0u};
+    }
+    if (smooth_k) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float f[8];
+        unpack8<T>(kw[i], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ks[e] += (double)f[e];
+      }
+    }
+    // V: per-row scale and e4m3 bytes. col_lo/col_hi[e] collect tokens 0..3 / 4..7 of column e.
+    uint32_t col_lo[8], col_hi[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) col_lo[e] = col_hi[e] = 0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t n = n0 + 8 * rg + i;
+      float f[8];
+      unpack8<T>(vw[i], f);
+      float vmax = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vmax = fmaxf(vmax, fabsf(f[e]));
+      vmax = max16(vmax);
+      const float sv = fmaxf(__fdiv_rn(vmax, P_SCALE), SCALE_FLOOR);
+      const bool live = n < N;
+      if (cg == 0 && n < N_pad) SV[bh * N_pad + n] = live ? sv : 0.0f;
+      if (live) sv_max = fmaxf(sv_max, sv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t byte = fp8x2(fminf(__fdiv_rn(f[e], sv), P_SCALE), 0.0f) & 0xffu;
+        if (i < 4)
+          col_lo[e] |= byte << (8 * i);
+        else
+          col_hi[e] |= byte << (8 * (i - 4));
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = 8 * cg + e;
+      const int pos = rg ^ cg;  // d >> 3 == cg
+      *(u32x2*)(tile + d * VT_STRIDE + 8 * pos) = (u32x2){col_lo[e], col_hi[e]};
+    }
+    __syncthreads();
+    {
+      const int d = tid >> 1, half = tid & 1, dx = d >> 3;
+      const int64_t nb = n0 + 64 * half;
+      if (nb < N_pad) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int r0 = 8 * half + 2 * m;  // token chunks r0, r0+1 (8 tokens each)
+          const int p0 = r0 ^ dx;
+          u32x4 x = *(const u32x4*)(tile + d * VT_STRIDE + 8 * (p0 & ~1));
+          if (p0 & 1) x = (u32x4){x.z, x.w, x.x, x.y};
+          *(u32x4*)(vt + (int64_t)d * N_pad + nb + 16 * m) = x;
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // fp64 mean partials: reduce the 16 row groups in a fixed order.
+  if (smooth_k) {
+    double* red = (double*)tile;  // 16 x 128 doubles = 16 KB <= sizeof(tile)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[rg * HD + 8 * cg + e] = ks[e];
+    __syncthreads();
+    if (tid < HD) {
+      double s = 0.0;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s += red[r * HD + tid];
+      part[(bh * C1 + c) * HD + tid] = s;
+    }
+  }
+  // block max of sv over live rows
+  float m = sv_max;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  if ((tid & 63) == 0) wmax[tid >> 6] = m;
+  __syncthreads();
+  if (tid == 0) smax[bh * C1 + c] = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+}
+
+// ---------------------------------------------------------------------------------------------
+// Quant pass. grid (C2, BH), block 256. Thread (cg, rg) handles row base+rg+16i, columns 8cg..+7.
+// ---------------------------------------------------------------------------------------------
+template <typename T, bool KINT8>
+__global__ __launch_bounds__(PT) void k_quant_kernel(
+    const T* __restrict__ K, u8* __restrict__ K8, float* __restrict__ SK, float* __restrict__ SV,
+    const double* __restrict__ part, const float* __restrict__ smax, float* __restrict__ MEAN,
+    float* __restrict__ S_out, int64_t H, int64_t N, int64_t N_pad, int64_t R2, int64_t C1,
+    int64_t k_sb, int64_t k_sh, int64_t k_sr, int smooth_k, int fold) {
+  __shared__ float mu_s[HD];
+  __shared__ float s_fold;
+
+  const int tid = threadIdx.x, cg = tid & 15, rg = tid >> 4;
+  const int64_t bh = blockIdx.y;
+  const int64_t b = bh / H, h = bh - b * H;
+
+  if (tid < HD) {
+    float mu = 0.0f;
+    if (smooth_k) {
+      double s = 0.0;
+      for (int64_t c = 0; c < C1; ++c) s += part[(bh * C1 + c) * HD + tid];
+      mu = (float)(s / (double)N);
+      if (MEAN != nullptr && blockIdx.x == 0) MEAN[bh * HD + tid] = mu;
+    }
+    mu_s[tid] = mu;
+  } else if (tid < HD + 64) {
+    const int l = tid - HD;
+    float m = 1.0f;
+    for (int64_t c = l; c < C1; c += 64) m = fmaxf(m, smax[bh * C1 + c]);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if (l == 0) {
+      s_fold = m;
+      if (blockIdx.x == 0) S_out[bh] = m;
+    }
+  }
+  __syncthreads();
+
+  float mu[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) mu[e] = mu_s[8 * cg + e];
+  const float S = s_fold;
+  const T* kp = K + b * k_sb + h * k_sh + 8 * cg;
+  const int64_t r_begin = (int64_t)blockIdx.x * R2;
+  const int64_t r_end = (r_begin + R2 < N_pad) ? r_begin + R2 : N_pad;
+
+  for (int64_t n0 = r_begin; n0 < r_end; n0 += 64) {
+    u32x4 kw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t n = n0 + rg + 16 * i;
+      kw[i] = (n < N) ? *(const u32x4*)(kp + n * k_sr) : (u32x4){0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t n = n0 + rg + 16 * i;
+      const bool live = n < N;
+      float kc[8];
+      unpack8<T>(kw[i], kc);
+      float kmax = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        kc[e] = live ? (smooth_k ? kc[e] - mu[e] : kc[e]) : 0.0f;
+        kmax = fmaxf(kmax, fabsf(kc[e]));
+      }
+      kmax = max16(kmax);
+      const float sk = fmaxf(__fdiv_rn(kmax, KINT8 ? I8_MAX : P_SCALE), SCALE_FLOOR);
+      if (n < r_end) {
+        u32x2 word;
+        if (KINT8) {
+          float x[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = __fdiv_rn(kc[e], sk);
+          word = (u32x2){i8x4(x[0], x[1], x[2], x[3]), i8x4(x[4], x[5], x[6], x[7])};
+        } else {
+          float x[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = fminf(__fdiv_rn(kc[e], sk), P_SCALE);
+          word = (u32x2){fp8x4(x[0], x[1], x[2], x[3]), fp8x4(x[4], x[5], x[6], x[7])};
+        }
+        *(u32x2*)(K8 + (bh * N_pad + n) * HD + 8 * cg) = word;
+        if (cg == 0) SK[bh * N_pad + n] = live ? sk : 1.0f;
+        if (cg == 1 && fold) SV[bh * N_pad + n] = __fdiv_rn(SV[bh * N_pad + n], S);
+      }
+    }
+  }
+}
+
+template <typename T>
+static hipError_t launch_prologue_t(const PrologueArgs& a, hipStream_t stream) {
+  const int64_t BH = a.B * a.H;
+  const PrologueGeom g = prologue_geom(BH, a.N_pad);
+  double* part = (double*)a.workspace;
+  const size_t part_bytes = ((size_t)BH * g.C1 * HD * sizeof(double) + 255) / 256 * 256;
+  float* smax = (float*)((char*)a.workspace + part_bytes);
+  hipLaunchKernelGGL(kv_stats_kernel<T>, dim3((unsigned)g.C1, (unsigned)BH), dim3(PT), 0, stream,
+                     (const T*)a.k, (const T*)a.v, (u8*)a.v8t, a.sv, part, smax, a.H, a.N, a.N_pad,
+                     g.R1, g.C1, a.k_sb, a.k_sh, a.k_sr, a.v_sb, a.v_sh, a.v_sr, a.smooth_k);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (a.k_int8)
+    hipLaunchKernelGGL((k_quant_kernel<T, true>), dim3((unsigned)g.C2, (unsigned)BH), dim3(PT), 0,
+                       stream, (const T*)a.k, (u8*)a.k8, a.sk, a.sv, part, smax, a.mean, a.s, a.H,
+                       a.N, a.N_pad, g.R2, g.C1, a.k_sb, a.k_sh, a.k_sr, a.smooth_k, a.fold);
+  else
+    hipLaunchKernelGGL((k_quant_kernel<T, false>), dim3((unsigned)g.C2, (unsigned)BH), dim3(PT), 0,
+                       stream, (const T*)a.k, (u8*)a.k8, a.sk, a.sv, part, smax, a.mean, a.s, a.H,
+                       a.N, a.N_pad, g.R2, g.C1, a.k_sb, a.k_sh, a.k_sr, a.smooth_k, a.fold);
+  return hipGetLastError();
+}
+
+hipError_t launch_prologue(const PrologueArgs& a, hipStream_t stream) {
+  return a.dtype == 1 ? launch_prologue_t<bf16>(a, stream) : launch_prologue_t<f16>(a, stream);
+}
+
+}  // namespace sage

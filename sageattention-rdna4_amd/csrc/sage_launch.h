@@ -1,0 +1,68 @@
+// Host-side launchers shared between the kernel translation units and the C ABI (capi.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace sage {
+
+// Geometry of the two-launch prologue for BH planes of N rows (N_pad = ceil(N/64)*64).
+//   stats pass: grid (C1, BH), each block owns R1 consecutive rows of one plane;
+//   quant pass: grid (ceil(N_pad/R2), BH), each block owns R2 rows.
+// Blocks are sized so that small calls still spread over the chip and large calls keep the
+// per-block mean-partial reduction short (C1 partials of 128 fp64 per plane).
+struct PrologueGeom {
+  int64_t R1, C1, R2, C2;
+};
+PrologueGeom prologue_geom(int64_t BH, int64_t N_pad);
+size_t prologue_workspace_bytes(int64_t BH, int64_t N_pad);
+
+struct PrologueArgs {
+  int dtype, k_int8, smooth_k, fold;
+  const void* k;
+  int64_t k_sb, k_sh, k_sr;
+  const void* v;
+  int64_t v_sb, v_sh, v_sr;
+  int64_t B, H, N, N_pad;
+  void* k8;
+  float* sk;
+  void* v8t;
+  float* sv;
+  float* mean;
+  float* s;
+  void* workspace;
+};
+hipError_t launch_prologue(const PrologueArgs& a, hipStream_t stream);
+
+struct AttnArgs {
+  int dtype, qk_int8, causal;
+  const void* q;
+  int64_t q_sb, q_sh, q_sr;
+  const void* k8;
+  const float* sk;
+  const void* v8t;
+  const float* sv;
+  const float* s;
+  void* o;
+  int64_t o_sb, o_sh, o_sr;
+  int64_t B, H, N, N_pad;
+  float sm_scale;
+};
+hipError_t launch_attn_fwd(const AttnArgs& a, hipStream_t stream);
+
+struct QuantQArgs {
+  int dtype, qk_int8;
+  const void* q;
+  int64_t q_sb, q_sh, q_sr;
+  int64_t B, H, N;
+  float sm_scale;
+  void* q8;
+  float* sq;
+  float* cq;
+};
+hipError_t launch_quant_q(const QuantQArgs& a, hipStream_t stream);
+
+hipError_t launch_layout_probe(const void* a, const void* bt, int32_t* c, const void* e,
+                               const void* ft, float* d, hipStream_t stream);
+
+}  // namespace sage

@@ -1,0 +1,200 @@
+"""The SK1 router on MI355X: envelope check, prologue, main loop.
+
+Mirrors `sageattention/sk1_backend/__init__.py` of the reference (`ENVELOPE` `:346-358`,
+`_envelope_ok` `:920-979`, `try_sk1_t1` `:982-1284`), re-designed for one backend:
+
+* one library (`libsagemi355.so`, gfx950) serves every call inside the envelope; there is no
+  fallback chain, no code-object selection and no backend switch;
+* fp16 inputs run int8 Q.K (the reference's `sk1_t6i`/`sk1_t6in`), bf16 inputs fp8 Q.K (the
+  reference's `sk1_t4a1sb`/`sk1_t4a1nb`); `int8=False` forces fp8 Q.K for fp16 inputs (the
+  reference's fp8 fp16 object), for comparisons;
+* contiguous HND, NHD and any other view the stride rule accepts take the same kernel (strides are
+  arguments), so NHD and fused-QKV views give the same bits as contiguous HND;
+* the per-(b,h) V-scale fold runs inside the prologue launch pair, not as three torch ops.
+
+`try_sk1_t1` keeps the reference's contract: `(out, None)` when served, `(None, reason)` when the
+call is outside the envelope or (with `strict=False`) when the library fails.
+"""
+import sys
+
+import torch
+
+from .hip_prologue import HipPrologue, n_pad_for  # noqa: F401
+from .sk1_loader import STRIDED_REFUSALS, SageLib, strided_view_reason  # noqa: F401
+
+#: The architectures the library is built for.
+SUPPORTED_ARCHS = ("gfx950",)
+
+#: What this build serves. `layout` HND or NHD; `contiguous` = any view `strided_view_reason`
+#: accepts (contiguous HND, physically-NHD, fused-QKV splits); head_dim 128 only.
+ENVELOPE = dict(
+    layout=("HND", "NHD"),
+    dtype=("fp16", "bf16"),
+    head_dim=(128,),
+    contiguous="any view strided_view_reason accepts",
+    causal=(0, 1),
+    smooth_k=(False, True),
+    batch_heads="B*H <= 65535",
+    seq_len="N >= 1",
+    return_lse=False,
+    attn_mask=False,
+    smooth_v=False,
+)
+
+_LOGGED = set()
+
+
+def _log_once(msg):
+    if msg not in _LOGGED:
+        _LOGGED.add(msg)
+        print("[sageattention-mi355] %s" % msg, file=sys.stderr)
+
+
+def device_arch(device=None) -> str:
+    """The device's `gcnArchName` prefix (before `:`), or "" if it cannot be read. Never raises.
+
+    A named module function so a test can monkeypatch the arch query
+    (`sageattention/sk1_backend/__init__.py:393-410` of the reference).
+    """
+    try:
+        if device is None:
+            device = torch.cuda.current_device()
+        name = getattr(torch.cuda.get_device_properties(device), "gcnArchName", "") or ""
+        return name.split(":", 1)[0]
+    except Exception:  # noqa: BLE001
+        return ""
+
+
+def arch_supported(device=None) -> bool:
+    return globals()["device_arch"](device) in SUPPORTED_ARCHS
+
+
+def _envelope_ok(q, k, v, tensor_layout, is_causal, sm_scale, return_lse, smooth_k, smooth_v,
+                 attn_mask):
+    """`None` when the call is served, else the refusal reason (the reference's strings,
+    `sageattention/sk1_backend/__init__.py:920-979`)."""
+    if tensor_layout not in ("HND", "NHD"):
+        return "layout"
+    if return_lse:
+        return "return_lse"
+    if attn_mask is not None:
+        return "attn_mask"
+    if smooth_v:
+        return "smooth_v"
+    if not (isinstance(q, torch.Tensor) and isinstance(k, torch.Tensor)
+            and isinstance(v, torch.Tensor)):
+        return "device"
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        return "device"
+    if q.device != k.device or q.device != v.device:
+        return "device"
+    if not (q.dtype == k.dtype == v.dtype):
+        return "dtype"
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        return "dtype"
+    if not (q.dim() == 4 and k.dim() == 4 and v.dim() == 4):
+        return "rank"
+    if tensor_layout == "NHD":
+        q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    for nm, t in (("q", q), ("k", k), ("v", v)):
+        r = strided_view_reason(t, nm)
+        if r is not None:
+            return r
+    if q.size(3) != 128 or k.size(3) != q.size(3) or v.size(3) != q.size(3):
+        return "head_dim"
+    if q.size(0) != k.size(0) or q.size(0) != v.size(0):
+        return "batch"
+    if q.size(1) != k.size(1) or q.size(1) != v.size(1):
+        return "heads"
+    if q.size(2) != k.size(2) or k.size(2) != v.size(2):
+        return "seq_len"
+    if q.size(2) < 1:
+        return "seq_len"
+    if q.size(0) * q.size(1) > 65535:
+        return "batch_heads"
+    return None
+
+
+def try_sk1_t1(q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=None, return_lse=False,
+               smooth_k=True, smooth_v=False, attn_mask=None, strict=False, int8=None, bf16=None):
+    """Run the gfx950 SK1 path if the call is inside `ENVELOPE`.
+
+    Returns `(out, None)` with `out` in the caller's layout and dtype, or `(None, reason)`.
+    `strict=True` raises instead of returning a refusal for a wrong arch or a library failure
+    (envelope misses are always returned as a reason). `int8=False` selects fp8 Q.K for fp16
+    inputs; `bf16` is accepted for signature compatibility (bf16 is always served).
+    """
+    del bf16
+    reason = _envelope_ok(q, k, v, tensor_layout, is_causal, sm_scale, return_lse, smooth_k,
+                          smooth_v, attn_mask)
+    if reason is not None:
+        return None, reason
+    if not arch_supported(q.device):
+        msg = ("device arch is %r; libsagemi355.so is built for %s"
+               % (device_arch(q.device) or "<unknown>", ", ".join(SUPPORTED_ARCHS)))
+        if strict:
+            raise RuntimeError(msg)
+        _log_once(msg)
+        return None, "arch"
+    try:
+        lib = SageLib.get()
+    except Exception as e:
+        if strict:
+            raise
+        _log_once("load failed: %s" % e)
+        return None, "load_failed"
+
+    try:
+        out = sk1_forward(lib, q, k, v, tensor_layout=tensor_layout, is_causal=is_causal,
+                          sm_scale=sm_scale, smooth_k=smooth_k, int8=int8)
+    except Exception as e:
+        if strict:
+            raise
+        _log_once("launch failed: %s" % e)
+        return None, "launch_failed"
+    return out, None
+
+
+def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=None,
+                smooth_k=True, int8=None, events=None):
+    """The served path without the envelope check: allocate, prologue (2 launches), main loop.
+
+    `events`, when given, is a sequence of three `torch.cuda.Event`s recorded on the launch stream
+    before the prologue, between the prologue and the main loop, and after the main loop.
+    """
+    if tensor_layout == "NHD":
+        qq, kk, vv = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    else:
+        qq, kk, vv = q, k, v
+    B, H, N, D = (int(x) for x in qq.shape)
+    BH = B * H
+    is_bf16 = q.dtype == torch.bfloat16
+    qk_int8 = (not is_bf16) and (int8 is None or bool(int8))
+    sm = float(sm_scale if sm_scale is not None else D ** -0.5)
+    n_pad = n_pad_for(N)
+    dev = q.device
+    k8 = torch.empty(BH, n_pad, D, device=dev,
+                     dtype=torch.int8 if qk_int8 else torch.float8_e4m3fn)
+    sk = torch.empty(BH, n_pad, device=dev, dtype=torch.float32)
+    v8t = torch.empty(BH, D, n_pad, device=dev, dtype=torch.float8_e4m3fn)
+    sv = torch.empty(BH, n_pad, device=dev, dtype=torch.float32)
+    s = torch.empty(BH, device=dev, dtype=torch.float32)
+    ws = torch.empty(lib.workspace_bytes(BH, N), device=dev, dtype=torch.uint8)
+    if tensor_layout == "NHD":
+        out = torch.empty(B, N, H, D, device=dev, dtype=q.dtype)
+        oo = out.transpose(1, 2)
+    else:
+        out = torch.empty(B, H, N, D, device=dev, dtype=q.dtype)
+        oo = out
+    with torch.cuda.device(dev):
+        if events is not None:
+            events[0].record()
+        lib.kv_prologue(kk, vv, k8, sk, v8t, sv, s, None, ws, k_int8=qk_int8,
+                        smooth_k=bool(smooth_k), fold=True, n_pad=n_pad)
+        if events is not None:
+            events[1].record()
+        lib.attn_fwd(qq, k8, sk, v8t, sv, s, oo, qk_int8=qk_int8, causal=bool(is_causal),
+                     sm_scale=sm, n_pad=n_pad)
+        if events is not None:
+            events[2].record()
+    return out

@@ -1,0 +1,177 @@
+"""ctypes binding of libsagemi355.so and the tensor contract of its launches.
+
+The reference binds prebuilt code objects through `hipModuleLoadData` on torch's HIP runtime
+(`sageattention/sk1_backend/sk1_loader.py:129-299` of the reference). This build instead loads one
+C-ABI shared library (`include/sage_mi355.h`) compiled for gfx950. `torch` is imported first, so the
+library's `libamdhip64.so.7` dependency resolves to the HIP runtime torch already loaded: one runtime
+image per process, and torch's stream handles are valid in the library.
+
+Every launch goes on `torch.cuda.current_stream()` with no host synchronization
+(`sk1_loader.py:17-19`, `:301-303` of the reference).
+"""
+import ctypes
+import os
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get(
+    "SAGE_MI355_LIB", os.path.join(os.path.dirname(_HERE), "_lib", "libsagemi355.so"))
+
+SAGE_F16, SAGE_BF16 = 0, 1
+
+#: Every reason `strided_view_reason` can return, in evaluation order. The strings are the
+#: reference's refusal vocabulary (`sageattention/sk1_backend/sk1_loader.py:308-309`).
+STRIDED_REFUSALS = ("rank", "stride_last", "stride_nonpos", "stride_align", "ptr_align",
+                    "stride_overlap", "stride_int32")
+_INT32_MAX = 2 ** 31 - 1
+
+
+def strided_view_reason(t, name="t"):
+    """`None` if `t` is a servable logical (B, H, N, D) view, else the refusal reason.
+
+    The rule of the reference (`sageattention/sk1_backend/sk1_loader.py:313-369`), restated from the
+    needs of this build's kernels, which read Q/K/V and write O with 16-byte vector accesses:
+    rank 4; last stride 1; every stride positive and the outer three multiples of 8 elements; a
+    16-byte-aligned pointer; an injective index map (sizes-1 dims dropped, strides sorted, each at
+    least the previous stride times its size); strides within int32.
+    """
+    if t.dim() != 4:
+        return "rank"
+    if int(t.stride(3)) != 1:
+        return "stride_last"
+    st = [int(s) for s in t.stride()]
+    if any(s <= 0 for s in st):
+        return "stride_nonpos"
+    if any(st[i] % 8 for i in (0, 1, 2)):
+        return "stride_align"
+    if int(t.data_ptr()) % 16:
+        return "ptr_align"
+    dims = sorted((st[i], int(t.shape[i])) for i in range(4) if int(t.shape[i]) > 1)
+    for (s0, n0), (s1, _) in zip(dims, dims[1:]):
+        if s1 < s0 * n0:
+            return "stride_overlap"
+    if any(s > _INT32_MAX for s in st):
+        return "stride_int32"
+    return None
+
+
+def torch_stream(device=None):
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _dtype_code(dt):
+    if dt == torch.float16:
+        return SAGE_F16
+    if dt == torch.bfloat16:
+        return SAGE_BF16
+    raise ValueError("dtype: %s is not served (fp16 and bf16 only)" % dt)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(0 if t is None else int(t.data_ptr()))
+
+
+class SageLib:
+    """The loaded library. `SageLib.get()` loads it once per process (under a lock) and raises
+    `RuntimeError` when it is missing or does not load: there is no other backend to fall back to."""
+
+    _instance = None
+    _lock = threading.Lock()
+
+    @classmethod
+    def get(cls):
+        if cls._instance is None:
+            with cls._lock:
+                if cls._instance is None:
+                    cls._instance = cls(LIB_PATH)
+        return cls._instance
+
+    def __init__(self, path):
+        if not os.path.isfile(path):
+            raise RuntimeError(
+                "the gfx950 library %s is not built (run `python sageattention-rdna4_amd/"
+                "build_lib.py` or `__graft_entry__.build()`)" % path)
+        self.path = path
+        self.lib = ctypes.CDLL(path, mode=ctypes.RTLD_GLOBAL)
+        L = self.lib
+        i64, f32, vp, i32 = ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_int
+        L.sage_version.restype = i32
+        L.sage_version.argtypes = []
+        L.sage_last_error.restype = ctypes.c_char_p
+        L.sage_last_error.argtypes = []
+        L.sage_kv_prologue_workspace_bytes.restype = ctypes.c_size_t
+        L.sage_kv_prologue_workspace_bytes.argtypes = [i64, i64]
+        L.sage_kv_prologue.restype = i32
+        L.sage_kv_prologue.argtypes = ([i32] * 4 + [vp, i64, i64, i64] * 2 + [i64] * 4
+                                       + [vp] * 7 + [ctypes.c_size_t, vp])
+        L.sage_attn_fwd.restype = i32
+        L.sage_attn_fwd.argtypes = ([i32] * 3 + [vp, i64, i64, i64] + [vp] * 5
+                                    + [vp, i64, i64, i64] + [i64] * 4 + [f32, vp])
+        L.sage_quant_q.restype = i32
+        L.sage_quant_q.argtypes = [i32, i32, vp, i64, i64, i64, i64, i64, i64, f32, vp, vp, vp, vp]
+        L.sage_mfma_layout_probe.restype = i32
+        L.sage_mfma_layout_probe.argtypes = [vp] * 7
+        self.version = int(L.sage_version())
+
+    # ------------------------------------------------------------------ helpers
+    def _check(self, rc, what):
+        if rc != 0:
+            msg = self.lib.sage_last_error().decode(errors="replace")
+            if rc == 1:
+                raise ValueError("%s: %s" % (what, msg))
+            raise RuntimeError("%s: %s" % (what, msg))
+
+    def workspace_bytes(self, BH, N):
+        return int(self.lib.sage_kv_prologue_workspace_bytes(int(BH), int(N)))
+
+    # ------------------------------------------------------------------ entry points
+    def kv_prologue(self, k, v, k8, sk, v8t, sv, s, mean, workspace, *, k_int8, smooth_k, fold,
+                    n_pad):
+        """K/V prologue on logical (B, H, N, D) views `k`, `v` (see `sage_kv_prologue`)."""
+        B, H, N, _ = (int(x) for x in k.shape)
+        rc = self.lib.sage_kv_prologue(
+            _dtype_code(k.dtype), int(bool(k_int8)), int(bool(smooth_k)), int(bool(fold)),
+            _ptr(k), k.stride(0), k.stride(1), k.stride(2),
+            _ptr(v), v.stride(0), v.stride(1), v.stride(2),
+            B, H, N, int(n_pad), _ptr(k8), _ptr(sk), _ptr(v8t), _ptr(sv), _ptr(mean), _ptr(s),
+            _ptr(workspace), int(workspace.numel() * workspace.element_size()),
+            ctypes.c_void_p(torch_stream(k.device)))
+        self._check(rc, "sage_kv_prologue")
+
+    def attn_fwd(self, q, k8, sk, v8t, sv, s, o, *, qk_int8, causal, sm_scale, n_pad):
+        """Main loop on logical (B, H, N, D) views `q`, `o` (see `sage_attn_fwd`)."""
+        B, H, N, _ = (int(x) for x in q.shape)
+        rc = self.lib.sage_attn_fwd(
+            _dtype_code(q.dtype), int(bool(qk_int8)), int(bool(causal)),
+            _ptr(q), q.stride(0), q.stride(1), q.stride(2),
+            _ptr(k8), _ptr(sk), _ptr(v8t), _ptr(sv), _ptr(s),
+            _ptr(o), o.stride(0), o.stride(1), o.stride(2),
+            B, H, N, int(n_pad), ctypes.c_float(float(sm_scale)),
+            ctypes.c_void_p(torch_stream(q.device)))
+        self._check(rc, "sage_attn_fwd")
+
+    def quant_q(self, q, sm_scale, *, qk_int8):
+        """Q quantized exactly as the main loop quantizes it: `(q8, sq, cq)` on q's device."""
+        B, H, N, D = (int(x) for x in q.shape)
+        dev = q.device
+        q8 = torch.empty(B * H, N, D, device=dev,
+                         dtype=torch.int8 if qk_int8 else torch.float8_e4m3fn)
+        sq = torch.empty(B * H, N, device=dev, dtype=torch.float32)
+        cq = torch.empty(B * H, N, device=dev, dtype=torch.float32)
+        rc = self.lib.sage_quant_q(
+            _dtype_code(q.dtype), int(bool(qk_int8)), _ptr(q), q.stride(0), q.stride(1),
+            q.stride(2), B, H, N, ctypes.c_float(float(sm_scale)), _ptr(q8), _ptr(sq), _ptr(cq),
+            ctypes.c_void_p(torch_stream(dev)))
+        self._check(rc, "sage_quant_q")
+        return q8, sq, cq
+
+    def layout_probe(self, a, bt, e, ft):
+        dev = a.device
+        c = torch.empty(32, 32, device=dev, dtype=torch.int32)
+        d = torch.empty(32, 32, device=dev, dtype=torch.float32)
+        rc = self.lib.sage_mfma_layout_probe(_ptr(a), _ptr(bt), _ptr(c), _ptr(e), _ptr(ft), _ptr(d),
+                                             ctypes.c_void_p(torch_stream(dev)))
+        self._check(rc, "sage_mfma_layout_probe")
+        return c, d

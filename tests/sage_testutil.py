@@ -1,0 +1,81 @@
+"""Shared helpers of the test suite: seeded CPU inputs, metrics, the gfx950 probe."""
+import functools
+
+import torch
+
+HEAD_DIM = 128
+
+
+@functools.lru_cache(maxsize=1)
+def have_gfx950():
+    if torch.version.hip is None or not torch.cuda.is_available():
+        return False
+    arch = getattr(torch.cuda.get_device_properties(0), "gcnArchName", "") or ""
+    return arch.split(":", 1)[0] == "gfx950"
+
+
+def make_qkv(b, h, n, *, seed=0, dtype=torch.float16, layout="HND", std=1.0, k_offset_std=0.0,
+             outlier_frac=0.0, outlier_scale=50.0, d=HEAD_DIM):
+    """Seeded CPU tensors, cast to `dtype` (the GPU and the oracle then see identical bytes).
+
+    Q, K, V ~ N(0, std). K gets a per-(b,h) channel offset mu ~ N(0, k_offset_std) broadcast over
+    tokens, and `round(outlier_frac * n)` K rows per plane (seeded choice) are scaled by
+    `outlier_scale` -- the synthetic inputs of the benchmark configurations.
+    Returns (q, k, v) in `layout` ("HND" (B,H,N,D) or "NHD" (B,N,H,D)), contiguous.
+    """
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, h, n, d, generator=g) * std
+    k = torch.randn(b, h, n, d, generator=g) * std
+    v = torch.randn(b, h, n, d, generator=g) * std
+    if k_offset_std:
+        k = k + torch.randn(b, h, 1, d, generator=g) * k_offset_std
+    n_out = int(round(outlier_frac * n))
+    if n_out:
+        for bi in range(b):
+            for hi in range(h):
+                idx = torch.randperm(n, generator=g)[:n_out]
+                k[bi, hi, idx] *= outlier_scale
+    out = [t.to(dtype) for t in (q, k, v)]
+    if layout == "NHD":
+        out = [t.transpose(1, 2).contiguous() for t in out]
+    return out
+
+
+def rel_rms(out, ref):
+    out, ref = out.double(), ref.double()
+    return ((out - ref).pow(2).mean().sqrt() / ref.pow(2).mean().sqrt()).item()
+
+
+def cosine(a, b):
+    a, b = a.double().flatten(), b.double().flatten()
+    return (a @ b / (a.norm() * b.norm())).item()
+
+
+def rel_l1(out, ref):
+    out, ref = out.double(), ref.double()
+    return ((out - ref).abs().sum() / ref.abs().sum()).item()
+
+
+def bytes_equal(a, b):
+    """Bitwise equality of two tensors of the same dtype (fp8 compared through uint8 views)."""
+    if a.dtype != b.dtype or a.shape != b.shape:
+        return False
+    if a.element_size() == 1:
+        return torch.equal(a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8))
+    if a.dtype == torch.float32:
+        return torch.equal(a.contiguous().view(torch.int32), b.contiguous().view(torch.int32))
+    return torch.equal(a, b)
+
+
+def mismatch_report(a, b, name):
+    a8 = a.contiguous().view(torch.uint8) if a.element_size() == 1 else a
+    b8 = b.contiguous().view(torch.uint8) if b.element_size() == 1 else b
+    if a.dtype == torch.float32:
+        a8, b8 = a.contiguous().view(torch.int32), b.contiguous().view(torch.int32)
+    diff = (a8 != b8)
+    n = int(diff.sum())
+    if n == 0:
+        return "%s: equal" % name
+    idx = diff.nonzero()[:5].tolist()
+    ex = [(i, a[tuple(i)].float().item(), b[tuple(i)].float().item()) for i in idx]
+    return "%s: %d/%d differ, e.g. %s" % (name, n, diff.numel(), ex)

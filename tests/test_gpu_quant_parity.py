@@ -1,0 +1,146 @@
+"""Bit-exact parity of the gfx950 quantizers with the CPU oracle (GPU tests).
+
+Every quantized tensor and scale of the scheme -- mu, K8, SK, V8T, SV, S, SV', Q8, sq, c_q -- must
+equal the oracle's bits. Outputs are prefilled with sentinels first, so a pad row the kernels fail
+to write shows up as a mismatch.
+"""
+import pytest
+import torch
+
+import oracle
+from sage_testutil import HEAD_DIM, bytes_equal, have_gfx950, make_qkv, mismatch_report
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not have_gfx950(), reason="needs a gfx950 GPU")]
+
+
+def _lib():
+    from sageattention.sk1_backend.sk1_loader import SageLib
+    return SageLib.get()
+
+
+def _run_prologue(k, v, *, k_int8, smooth_k, fold, layout="HND"):
+    lib = _lib()
+    kk, vv = (oracle.to_hnd(t, layout) for t in (k, v))
+    B, H, N, D = kk.shape
+    BH = B * H
+    n_pad = oracle.n_pad_for(N)
+    dev = k.device
+    k8 = torch.full((BH, n_pad, D), 0x5A, device=dev, dtype=torch.uint8)
+    k8 = k8.view(torch.int8 if k_int8 else torch.float8_e4m3fn)
+    v8t = torch.full((BH, D, n_pad), 0x5A, device=dev, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    sk = torch.full((BH, n_pad), float("nan"), device=dev)
+    sv = torch.full((BH, n_pad), float("nan"), device=dev)
+    s = torch.full((BH,), float("nan"), device=dev)
+    mean = torch.full((BH, D), float("nan"), device=dev)
+    ws = torch.full((lib.workspace_bytes(BH, N),), 0xFF, device=dev, dtype=torch.uint8)
+    lib.kv_prologue(kk, vv, k8, sk, v8t, sv, s, mean, ws, k_int8=k_int8, smooth_k=smooth_k,
+                    fold=fold, n_pad=n_pad)
+    torch.cuda.synchronize()
+    return dict(k8=k8.cpu(), sk=sk.cpu(), v8t=v8t.cpu(), sv=sv.cpu(), s=s.cpu(), mean=mean.cpu())
+
+
+def _oracle_prologue(k, v, *, k_int8, smooth_k, layout="HND"):
+    kk, vv = (oracle.to_hnd(t, layout) for t in (k, v))
+    B, H, N, D = kk.shape
+    kr, vr = kk.reshape(B * H, N, D), vv.reshape(B * H, N, D)
+    n_pad = oracle.n_pad_for(N)
+    mean = oracle.kseq_mean(kr) if smooth_k else None
+    k8, sk = oracle.quant_k(kr, n_pad, mean=mean, int8=k_int8)
+    v8t, sv = oracle.quant_v(vr, n_pad)
+    s, svp = oracle.fold_v_scale(sv)
+    return dict(mean=mean, k8=k8, sk=sk, v8t=v8t, sv=sv, s=s, svp=svp)
+
+
+CASES = [
+    # (dtype, k_int8, N, H, k_offset, outliers, std)
+    (torch.float16, True, 1, 2, 2.0, 0.0, 1.0),
+    (torch.float16, True, 63, 2, 2.0, 0.0, 1.0),
+    (torch.float16, True, 64, 3, 2.0, 0.0, 1.0),
+    (torch.float16, True, 65, 2, 2.0, 0.0, 1.0),
+    (torch.float16, True, 300, 2, 2.0, 0.01, 1.0),
+    (torch.float16, True, 1000, 4, 2.0, 0.001, 1.0),
+    (torch.float16, True, 8771, 2, 2.0, 0.001, 1.0),
+    (torch.float16, False, 300, 2, 2.0, 0.0, 1.0),
+    (torch.bfloat16, False, 1, 2, 2.0, 0.0, 1.5),
+    (torch.bfloat16, False, 129, 2, 2.0, 0.0, 1.5),
+    (torch.bfloat16, False, 1000, 3, 2.0, 0.001, 1.5),
+    (torch.bfloat16, False, 16384, 1, 2.0, 0.001, 1.5),
+]
+
+
+@pytest.mark.parametrize("smooth_k", [True, False])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "%s-%s-N%d" % (
+    str(c[0]).split(".")[-1], "i8" if c[1] else "f8", c[2]))
+def test_prologue_bit_exact(case, smooth_k):
+    dtype, k_int8, N, H, off, outl, std = case
+    q, k, v = make_qkv(1, H, N, seed=N + H, dtype=dtype, std=std, k_offset_std=off,
+                       outlier_frac=outl)
+    print("case", case, "smooth_k", smooth_k, flush=True)
+    ref = _oracle_prologue(k, v, k_int8=k_int8, smooth_k=smooth_k)
+    got = _run_prologue(k.cuda(), v.cuda(), k_int8=k_int8, smooth_k=smooth_k, fold=False)
+    if smooth_k:
+        assert bytes_equal(got["mean"], ref["mean"]), mismatch_report(got["mean"], ref["mean"], "mean")
+    for name in ("k8", "sk", "v8t", "sv", "s"):
+        assert bytes_equal(got[name], ref[name]), mismatch_report(got[name], ref[name], name)
+    folded = _run_prologue(k.cuda(), v.cuda(), k_int8=k_int8, smooth_k=smooth_k, fold=True)
+    assert bytes_equal(folded["sv"], ref["svp"]), mismatch_report(folded["sv"], ref["svp"], "svp")
+    assert bytes_equal(folded["k8"], ref["k8"])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prologue_v_outlier_fold(dtype):
+    # |V| far above 448 makes S > 1, so SV' = SV / S differs from SV (the reference's outlier case).
+    q, k, v = make_qkv(1, 2, 1024, seed=1, dtype=dtype)
+    v[:, :, 300] = 20000.0
+    k_int8 = dtype == torch.float16
+    ref = _oracle_prologue(k, v, k_int8=k_int8, smooth_k=True)
+    assert (ref["s"] > 1).all()
+    got = _run_prologue(k.cuda(), v.cuda(), k_int8=k_int8, smooth_k=True, fold=True)
+    for name, rname in (("k8", "k8"), ("sk", "sk"), ("v8t", "v8t"), ("sv", "svp"), ("s", "s")):
+        assert bytes_equal(got[name], ref[rname]), mismatch_report(got[name], ref[rname], name)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prologue_strided_views_same_bits(dtype):
+    # NHD input read through strides gives the same bytes as contiguous HND.
+    q, k, v = make_qkv(2, 4, 300, seed=3, dtype=dtype, k_offset_std=2.0)
+    k_int8 = dtype == torch.float16
+    a = _run_prologue(k.cuda(), v.cuda(), k_int8=k_int8, smooth_k=True, fold=True)
+    kn, vn = (t.transpose(1, 2).contiguous().cuda() for t in (k, v))
+    b = _run_prologue(kn, vn, k_int8=k_int8, smooth_k=True, fold=True, layout="NHD")
+    for name in ("k8", "sk", "v8t", "sv", "s", "mean"):
+        assert bytes_equal(a[name], b[name]), name
+
+
+@pytest.mark.parametrize("dtype,qk_int8", [(torch.float16, True), (torch.float16, False),
+                                           (torch.bfloat16, False)])
+@pytest.mark.parametrize("N", [1, 31, 33, 300, 4097])
+def test_quant_q_bit_exact(dtype, qk_int8, N):
+    q, k, v = make_qkv(1, 3, N, seed=7 + N, dtype=dtype, std=1.5)
+    q[0, 1, : min(N, 5)] = 0.0          # all-zero rows take the 1e-12 floor
+    if N > 10:
+        q[0, 2, 7, 3] = 60000.0 if dtype == torch.float16 else 3.0e5   # a huge element
+    sm = HEAD_DIM ** -0.5
+    q8, sq, cq = _lib().quant_q(q.cuda(), sm, qk_int8=qk_int8)
+    torch.cuda.synchronize()
+    r8, rsq, rcq = oracle.quant_q(q.reshape(3, N, HEAD_DIM), sm, int8=qk_int8)
+    assert bytes_equal(q8.cpu(), r8), mismatch_report(q8.cpu(), r8, "q8")
+    assert bytes_equal(sq.cpu(), rsq), mismatch_report(sq.cpu(), rsq, "sq")
+    assert bytes_equal(cq.cpu(), rcq), mismatch_report(cq.cpu(), rcq, "cq")
+
+
+def test_fp8_convert_matches_torch_on_all_fp16_in_range():
+    # Every finite fp16 value with |x| <= 448 quantized as a V row with sv = 1: e4m3(min(x/1, 448))
+    # must equal torch's float8_e4m3fn cast, i.e. the hardware convert is OCP e4m3fn with RNE.
+    allv = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16).view(torch.float16)
+    vals = allv[torch.isfinite(allv) & (allv.float().abs() <= 448)]
+    n = vals.numel() // HEAD_DIM * HEAD_DIM
+    vals = vals[:n].reshape(1, 1, n // HEAD_DIM, HEAD_DIM).clone()
+    vals[..., 0] = 448.0                  # every row's absmax is 448, so sv == 1 exactly
+    k = torch.zeros_like(vals)
+    got = _run_prologue(k.cuda(), vals.cuda(), k_int8=True, smooth_k=False, fold=False)
+    rows = vals.shape[2]
+    ref = vals.reshape(rows, HEAD_DIM).float().to(torch.float8_e4m3fn).t()
+    assert (got["sv"][0, :rows] == 1.0).all()
+    assert bytes_equal(got["v8t"][0, :, :rows].contiguous(), ref.contiguous())
