@@ -1,0 +1,136 @@
+"""Host-side tests (CPU, no GPU): the C-ABI library exports, the stride rule, the envelope, and the
+drop-in `sageattn`'s error behaviour."""
+import ctypes
+import inspect
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sage_mi355.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(sage_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_entry_points():
+    syms = _declared_symbols()
+    for s in ("sage_version", "sage_last_error", "sage_kv_prologue_workspace_bytes",
+              "sage_kv_prologue", "sage_attn_fwd", "sage_quant_q", "sage_mfma_layout_probe"):
+        assert s in syms
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    from sageattention.sk1_backend import sk1_loader
+    if not os.path.isfile(sk1_loader.LIB_PATH):
+        pytest.skip("library not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(sk1_loader.LIB_PATH)
+    for s in _declared_symbols():
+        assert hasattr(lib, s), s
+    out = subprocess.run(["nm", "-D", "--defined-only", sk1_loader.LIB_PATH], capture_output=True,
+                         text=True).stdout
+    exported = set(re.findall(r" T (sage_\w+)", out))
+    assert exported == set(_declared_symbols())
+
+
+def test_library_host_calls_without_a_gpu():
+    # Calls that touch no device: the version, the workspace size, and argument refusals (which
+    # are checked before any launch).
+    from sageattention.sk1_backend import sk1_loader
+    if not os.path.isfile(sk1_loader.LIB_PATH):
+        pytest.skip("library not built")
+    L = sk1_loader.SageLib.get()
+    assert L.version >= 100
+    assert L.workspace_bytes(48, 47520) > 48 * 128 * 8
+    assert L.workspace_bytes(1, 1) > 0
+    i64 = ctypes.c_int64
+    rc = L.lib.sage_attn_fwd(0, 1, 1, None, 8, 8, 8, None, None, None, None, None, None, 8, 8, 8,
+                             1, 1, 0, 64, ctypes.c_float(0.1), None)
+    assert rc == 1 and b"n_lt_1" in L.lib.sage_last_error()
+    rc = L.lib.sage_kv_prologue(1, 1, 1, 1, None, 8, 8, 8, None, 8, 8, 8, 1, 1, 10, 64,
+                                *([None] * 7), 0, None)
+    assert rc == 1 and b"bf16_int8" in L.lib.sage_last_error()
+    rc = L.lib.sage_kv_prologue(0, 1, 1, 1, ctypes.c_void_p(16), 8, 8, 4, ctypes.c_void_p(16),
+                                8, 8, 8, 1, 1, 10, 64, *([None] * 7), 0, None)
+    assert rc == 1 and b"stride_align" in L.lib.sage_last_error()
+    rc = L.lib.sage_attn_fwd(0, 1, 0, ctypes.c_void_p(16), 8, 8, 8, None, None, None, None, None,
+                             ctypes.c_void_p(16), 8, 8, 8, 1, 1, 100, 96, ctypes.c_float(0.1), None)
+    assert rc == 1 and b"n_pad" in L.lib.sage_last_error()
+
+
+def test_strided_view_reason_rule():
+    from sageattention.sk1_backend.sk1_loader import strided_view_reason as r
+    t = torch.empty(2, 4, 100, 128, dtype=torch.float16)
+    assert r(t) is None
+    assert r(t.transpose(1, 2).contiguous().transpose(1, 2)) is None        # physically NHD
+    assert r(t[..., :64]) is None
+    assert r(t[:, :, :, 1:65]) == "ptr_align"
+    assert r(t.transpose(2, 3)) == "stride_last"
+    assert r(t[0]) == "rank"
+    assert r(t.expand(2, 4, 100, 128).as_strided((2, 4, 100, 128), (0, 12800, 128, 1))) == "stride_nonpos"
+    assert r(torch.empty(1, 1, 4, 136, dtype=torch.float16)[..., :128]) is None
+    assert r(torch.empty(1, 1, 4, 132, dtype=torch.float16)[..., :128]) == "stride_align"
+    over = torch.empty(4096, dtype=torch.float16).as_strided((1, 2, 10, 128), (2048, 64, 128, 1))
+    assert r(over) == "stride_overlap"
+    # fused QKV split: row stride 3*H*D, B=1 via unsqueeze (size-1 dims are ignored)
+    qkv = torch.empty(100, 3 * 4 * 128, dtype=torch.float16)
+    q = qkv.split(4 * 128, dim=-1)[1].view(100, 4, 128).transpose(0, 1).unsqueeze(0)
+    assert r(q) is None
+
+
+def test_envelope_reasons_on_cpu_tensors():
+    from sageattention.sk1_backend import _envelope_ok
+    q = torch.empty(1, 2, 10, 128, dtype=torch.float16)
+    args = dict(tensor_layout="HND", is_causal=False, sm_scale=None, return_lse=False,
+                smooth_k=True, smooth_v=False, attn_mask=None)
+    assert _envelope_ok(q, q, q, **dict(args, tensor_layout="BHND")) == "layout"
+    assert _envelope_ok(q, q, q, **dict(args, return_lse=True)) == "return_lse"
+    assert _envelope_ok(q, q, q, **dict(args, smooth_v=True)) == "smooth_v"
+    assert _envelope_ok(q, q, q, **dict(args, attn_mask=torch.ones(1))) == "attn_mask"
+    assert _envelope_ok(q, q, q, **args) == "device"
+
+
+def test_sageattn_signature_and_refusals():
+    from sageattention import sageattn
+    params = list(inspect.signature(sageattn).parameters)
+    assert params[:7] == ["q", "k", "v", "tensor_layout", "is_causal", "sm_scale", "return_lse"]
+    assert "attn_mask" not in params                   # ComfyUI probes for its absence
+    q = torch.empty(1, 2, 10, 128, dtype=torch.float16)
+    with pytest.raises(NotImplementedError):
+        sageattn(q, q, q, attn_mask=torch.ones(1))
+    with pytest.raises(ValueError, match="device"):
+        sageattn(q, q, q)
+    with pytest.raises(TypeError):
+        sageattn(q, q, q, no_such_kwarg=1)
+
+
+def test_try_sk1_t1_returns_reasons():
+    from sageattention.sk1_backend import try_sk1_t1
+    q = torch.empty(1, 2, 10, 128, dtype=torch.float16)
+    assert try_sk1_t1(q, q, q) == (None, "device")
+    assert try_sk1_t1(q, q, q, return_lse=True) == (None, "return_lse")
+
+
+def test_arch_gate_is_monkeypatchable(monkeypatch):
+    import sageattention.sk1_backend as sk1
+    monkeypatch.setattr(sk1, "device_arch", lambda device=None: "gfx942")
+    assert not sk1.arch_supported(None)
+    monkeypatch.setattr(sk1, "device_arch", lambda device=None: "gfx950")
+    assert sk1.arch_supported(None)
+
+
+def test_product_path_has_no_oracle_or_cpu_fallback():
+    # The shipped package never imports the test oracle, and has no torch-only attention path.
+    pkg = os.path.join(ROOT, "sageattention-rdna4_amd", "sageattention")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith(".py"):
+                src = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in src, f
+                assert "scaled_dot_product_attention" not in src, f

@@ -1,0 +1,302 @@
+"""Pins of the CPU oracle (CPU tests, no GPU).
+
+The oracle is the checker of every GPU parity test, so it is itself checked against things that do
+not share its code: exact rational arithmetic (`exact_ref`), an OCP e4m3 encoder written from the
+specification, Python's own half-even rounding, `math.fsum`, brute-force loops on tiny inputs, and
+closed forms of attention. A few tests plant a plausible mistake in a copy of an oracle function and
+assert that the pin catches it.
+"""
+import math
+import random
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from exact_ref import e4m3_code, e4m3_value, f32_bits, rn32, rne_int
+from sage_testutil import make_qkv
+
+F8 = torch.float8_e4m3fn
+
+
+# ----------------------------------------------------------------------------- n_pad
+def test_n_pad_closed_form():
+    table = {1: 64, 63: 64, 64: 64, 65: 128, 288: 320, 1024: 1024, 8771: 8832, 16384: 16384,
+             47520: 47552}
+    for n, p in table.items():
+        assert oracle.n_pad_for(n) == p
+    for n in range(1, 1000):
+        p = oracle.n_pad_for(n)
+        assert p % 64 == 0 and p >= n and p - n < 64
+
+
+# ----------------------------------------------------------------------------- rounding rules
+def test_torch_round_is_half_even():
+    xs = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, 127.5, -127.5, -128.5, 3.4999998, 0.49999997]
+    got = torch.round(torch.tensor(xs, dtype=torch.float32)).tolist()
+    assert got == [float(rne_int(Fraction(x))) for x in xs]
+    assert got[:6] == [0.0, 2.0, 2.0, -0.0, -2.0, -2.0]
+
+
+def test_reference_floor_rne_formula_equals_half_even():
+    # The reference's int8 K rounding is floor-based (`kernels/hip/h34_prologue.hip:56-64`):
+    # fl = floor(x); d = x - fl; q = (d > .5 or (d == .5 and fl odd)) ? fl + 1 : fl, in fp32.
+    # Restated with numpy fp32 scalars, it must equal half-even rounding on every fp32 x, including
+    # the (-1, 0) range where x - fl is inexact.
+    rng = random.Random(0)
+    xs = [k / 2 for k in range(-300, 301)]
+    xs += [rng.uniform(-130, 130) for _ in range(20000)]
+    xs += [float(np.nextafter(np.float32(k / 2), np.float32(s))) for k in range(-260, 261)
+           for s in (-1e9, 1e9)]
+    xs += [-0.5 + 2.0 ** -25, -0.5 - 2.0 ** -25, -2.0 ** -30, -1 + 2.0 ** -24]
+    for x in xs:
+        x32 = np.float32(x)
+        fl = np.floor(x32)
+        d = np.float32(x32 - fl)
+        odd = int(fl) & 1
+        q = fl + 1 if (d > 0.5 or (d == 0.5 and odd)) else fl
+        assert float(q) == float(rne_int(Fraction(float(x32)))), x
+
+
+# ----------------------------------------------------------------------------- e4m3
+def _torch_e4m3_codes(xs):
+    return torch.tensor(xs, dtype=torch.float32).to(F8).view(torch.uint8).tolist()
+
+
+def test_e4m3_cast_matches_ocp_encoder_on_every_fp16_in_range():
+    allv = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16).view(torch.float16)
+    vals = allv[torch.isfinite(allv) & (allv.float().abs() <= 448)].float()
+    got = vals.to(F8).view(torch.uint8).tolist()
+    want = [e4m3_code(float(x)) for x in vals.tolist()]
+    assert got == want
+
+
+def test_e4m3_cast_ties_and_boundaries():
+    xs, want = [], []
+    # every midpoint between consecutive positive codes, and one fp32 ulp either side of it
+    for c in range(0, 0x7E):
+        lo, hi = e4m3_value(c), e4m3_value(c + 1)
+        mid = (lo + hi) / 2
+        for x in (float(mid), float(np.nextafter(np.float32(mid), np.float32(0))),
+                  float(np.nextafter(np.float32(mid), np.float32(1e9)))):
+            xs += [x, -x]
+    xs += [448.0, 449.0, 463.99997, 1.0625, 1.1875, 2.0 ** -10, 3 * 2.0 ** -10, 2.0 ** -9]
+    want = [e4m3_code(Fraction(x)) for x in xs]
+    assert _torch_e4m3_codes(xs) == want
+    assert _torch_e4m3_codes([1.0625, 1.1875, 2.0 ** -10, 3 * 2.0 ** -10]) == [0x38, 0x3A, 0x00, 0x02]
+
+
+# ----------------------------------------------------------------------------- exact pins
+def _rn32_div(a, b):
+    return rn32(Fraction(a) / Fraction(b))
+
+
+def _k_int8_exact(row, mu=None):
+    """Exact restatement of A.3 for one row: returns (sk, [k8])."""
+    kc = [rn32(Fraction(float(x)) - Fraction(float(m))) if mu is not None else float(x)
+          for x, m in zip(row, mu if mu is not None else row)]
+    kmax = max(abs(x) for x in kc)
+    sk = max(_rn32_div(kmax, 127), float(np.float32(1e-12)))
+    k8 = [max(-128, min(127, rne_int(_rn32_div(x, sk)))) for x in kc]
+    return sk, k8
+
+
+def test_quant_k_int8_exact_small():
+    q, k, v = make_qkv(1, 2, 37, seed=3, k_offset_std=2.0, outlier_frac=0.05)
+    kr = k.reshape(2, 37, 128)
+    mean = oracle.kseq_mean(kr)
+    k8, sk = oracle.quant_k(kr, 64, mean=mean, int8=True)
+    for bh in range(2):
+        mu = mean[bh].tolist()
+        for n in range(37):
+            s_ex, q_ex = _k_int8_exact(kr[bh, n].float().tolist(), mu)
+            assert f32_bits(sk[bh, n].item()) == f32_bits(s_ex)
+            assert k8[bh, n].tolist() == q_ex
+        assert (sk[bh, 37:] == 1.0).all() and (k8[bh, 37:] == 0).all()
+
+
+def test_quant_k_int8_is_a_division_not_a_reciprocal_product():
+    # Plant the mistake "kc * RN(1/sk)" in a copy of the quantizer: on these inputs it changes
+    # some bytes, so the exact pin above would catch it.
+    q, k, v = make_qkv(1, 4, 256, seed=11)
+    kr = k.reshape(4, 256, 128)
+    k8, sk = oracle.quant_k(kr, 256, int8=True)
+    kf = kr.float()
+    wrong = torch.clamp(torch.round(kf * (1.0 / sk[:, :, None])), -128, 127).to(torch.int8)
+    assert not torch.equal(wrong, k8)
+    rows = [(b, n) for b in range(4) for n in range(256) if not torch.equal(wrong[b, n], k8[b, n])]
+    b, n = rows[0]
+    s_ex, q_ex = _k_int8_exact(kr[b, n].float().tolist())
+    assert k8[b, n].tolist() == q_ex and wrong[b, n].tolist() != q_ex
+
+
+def test_quant_k_fp8_and_v_exact_small():
+    q, k, v = make_qkv(1, 1, 20, seed=5, dtype=torch.bfloat16, std=1.5, k_offset_std=2.0)
+    kr, vr = k.reshape(1, 20, 128), v.reshape(1, 20, 128)
+    k8, sk = oracle.quant_k(kr, 64, int8=False)
+    v8t, sv = oracle.quant_v(vr, 64)
+    fl = float(np.float32(1e-12))
+    for n in range(20):
+        row = [float(x) for x in kr[0, n].float().tolist()]
+        s_ex = max(_rn32_div(max(abs(x) for x in row), 448), fl)
+        assert f32_bits(sk[0, n].item()) == f32_bits(s_ex)
+        want = [e4m3_code(min(Fraction(_rn32_div(x, s_ex)), Fraction(448))) for x in row]
+        assert k8[0, n].view(torch.uint8).tolist() == want
+        vrow = [float(x) for x in vr[0, n].float().tolist()]
+        sv_ex = max(_rn32_div(max(abs(x) for x in vrow), 448), fl)
+        assert f32_bits(sv[0, n].item()) == f32_bits(sv_ex)
+        wantv = [e4m3_code(min(Fraction(_rn32_div(x, sv_ex)), Fraction(448))) for x in vrow]
+        assert v8t[0, :, n].contiguous().view(torch.uint8).tolist() == wantv
+    assert (sv[0, 20:] == 0).all() and (v8t[0, :, 20:].view(torch.uint8) == 0).all()
+
+
+def test_quant_q_exact_small():
+    # Q uses a multiplication by the correctly rounded reciprocal (`sk1_t6i.hip:108`, `:115`).
+    q, k, v = make_qkv(1, 1, 24, seed=9, std=1.3)
+    qr = q.reshape(1, 24, 128)
+    sm = 128 ** -0.5
+    for int8 in (True, False):
+        q8, sq, cq = oracle.quant_q(qr, sm, int8=int8)
+        top = 127 if int8 else 448
+        smlog = rn32(Fraction(float(np.float32(sm))) * Fraction(float(np.float32(1.4426950408889634))))
+        for n in range(24):
+            row = [float(x) for x in qr[0, n].float().tolist()]
+            amax = max(max(abs(x) for x in row), float(np.float32(1e-12)))
+            qinv = _rn32_div(top, amax)
+            s_ex = _rn32_div(amax, top)
+            assert f32_bits(sq[0, n].item()) == f32_bits(s_ex)
+            assert f32_bits(cq[0, n].item()) == f32_bits(rn32(Fraction(smlog) * Fraction(s_ex)))
+            prod = [rn32(Fraction(x) * Fraction(qinv)) for x in row]
+            if int8:
+                assert q8[0, n].tolist() == [max(-128, min(127, rne_int(p))) for p in prod]
+            else:
+                want = [e4m3_code(max(min(Fraction(p), Fraction(448)), Fraction(-448))) for p in prod]
+                assert q8[0, n].view(torch.uint8).tolist() == want
+
+
+def test_kseq_mean_matches_fsum_and_is_order_free():
+    q, k, v = make_qkv(1, 3, 301, seed=2, k_offset_std=2.0)
+    kr = k.reshape(3, 301, 128)
+    mean = oracle.kseq_mean(kr)
+    for bh in range(3):
+        for d in (0, 17, 127):
+            col = [float(x) for x in kr[bh, :, d].float().tolist()]
+            s = math.fsum(col)                        # exact here: the sum is representable
+            assert Fraction(s) == sum(Fraction(x) for x in col)
+            want = float(np.float32(s / 301.0))      # RN64 of s/N, then RN32 (the reference's)
+            assert f32_bits(mean[bh, d].item()) == f32_bits(want)
+    perm = torch.randperm(301, generator=torch.Generator().manual_seed(0))
+    assert torch.equal(oracle.kseq_mean(kr[:, perm]), mean)
+
+
+def test_fold_v_scale_closed_form():
+    sv = torch.tensor([[0.5, 0.25, 0.0], [3.0, 1.5, 0.0]], dtype=torch.float32)
+    s, svp = oracle.fold_v_scale(sv)
+    assert s.tolist() == [1.0, 3.0]
+    assert torch.equal(svp[0], sv[0])                  # S == 1: SV' is SV bit for bit
+    assert f32_bits(svp[1, 1].item()) == f32_bits(rn32(Fraction(1.5) / 3))
+
+
+# ----------------------------------------------------------------------------- attention
+def _brute_force_row(q8r, cqr, k8, sk, v8t, svp, S, row, N, causal, int8, tile=64):
+    """One output row of A.9-A.11 in numpy fp32 scalars with Python loops (no torch)."""
+    f32 = np.float32
+    n_pad = k8.shape[0]
+    qv = q8r.astype(np.float64)
+    m, l = f32(-np.inf), f32(0)
+    acc = np.zeros(128, dtype=np.float32)
+    for j0 in range(0, n_pad, tile):
+        s = []
+        for n in range(j0, j0 + tile):
+            dot = f32(float(np.dot(qv, k8[n].astype(np.float64))))
+            val = f32(dot * f32(cqr * sk[n]))
+            dead = (n > row) if causal else (n >= N)
+            s.append(f32(-np.inf) if dead else val)
+        m_new = f32(max(m, max(s)))
+        m_use = f32(0) if m_new == -np.inf else m_new
+        alpha = f32(2.0 ** float(f32(m - m_use)))
+        p = [f32(2.0 ** float(f32(x - m_use))) for x in s]
+        psum = f32(0)
+        for x in p:
+            psum = f32(psum + x)
+        l = f32(f32(l * alpha) + psum)
+        acc = (acc * alpha).astype(np.float32)
+        for i, n in enumerate(range(j0, j0 + tile)):
+            p8 = float(e4m3_value(e4m3_code(Fraction(float(f32(p[i] * f32(svp[n] * f32(448))))))))
+            acc = (acc + np.float32(p8) * v8t[:, n].astype(np.float32)).astype(np.float32)
+        m = m_new
+    inv = f32(S / f32(l * f32(448))) if l > 0 else f32(0)
+    return (acc * inv).astype(np.float32)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("N", [5, 64, 130])
+def test_attention_tiles_vs_brute_force(N, causal):
+    q, k, v = make_qkv(1, 1, N, seed=N, k_offset_std=1.0)
+    r = oracle.emulate_sageattn(q, k, v, is_causal=causal)
+    k8 = r["k8"][0].numpy().astype(np.int32)
+    v8t = r["v8t"][0].float().numpy()
+    q8 = r["q8"][0].numpy().astype(np.int32)
+    out = r["o"][0, 0].float().numpy()
+    for row in sorted({0, 1, N // 2, N - 1}):
+        want = _brute_force_row(q8[row], r["c_q"][0, row].item(), k8, r["sk"][0].numpy(), v8t,
+                                r["svp"][0].numpy(), r["s"][0].item(), row, N, causal, True)
+        got = out[row]
+        assert np.allclose(got, want.astype(np.float16).astype(np.float32), rtol=2e-3, atol=2e-4), row
+
+
+def test_causal_first_row_closed_form():
+    # Row 0 of a causal call sees only key 0: p = exp2(0) = 1 exactly, so
+    # O[0] = fp16( e4m3(RN(SV'[0]*448)) * V8[0] * RN(S / RN(1*448)) ).
+    q, k, v = make_qkv(1, 2, 70, seed=4)
+    v[0, 1, 0] *= 3000.0                       # plane 1: |V| > 448, so S > 1 there
+    r = oracle.emulate_sageattn(q, k, v, is_causal=True)
+    for bh in range(2):
+        svp0, S = Fraction(r["svp"][bh, 0].item()), Fraction(r["s"][bh].item())
+        p8 = e4m3_value(e4m3_code(rn32(rn32(svp0 * 448))))
+        inv = rn32(S / rn32(Fraction(448)))
+        v8 = [e4m3_value(c) for c in r["v8t"][bh, :, 0].contiguous().view(torch.uint8).tolist()]
+        want = torch.tensor([rn32(rn32(p8 * x) * Fraction(inv)) for x in v8]).half()
+        assert torch.equal(r["o"][0, bh, 0], want)
+    assert r["s"][1].item() > 1.0
+
+
+def test_uniform_keys_give_the_mean_of_v():
+    # Identical keys: every score is equal, so the output is the (quantized) mean of V.
+    q, k, v = make_qkv(1, 1, 200, seed=6)
+    k[:] = k[:, :, :1]
+    r = oracle.emulate_sageattn(q, k, v, is_causal=False, smooth_k=False)
+    mean_v = v[0, 0].float().mean(0)
+    assert (r["o"][0, 0].float() - mean_v).abs().max().item() < 0.02
+
+
+def test_emulation_close_to_exact_attention():
+    # The scheme's error against exact attention on N(0,1) inputs: the reference's bar is 0.08
+    # relative RMS (`tests/test_sk1_backend.py:28-29`), observed 0.03-0.055.
+    for dtype in (torch.float16, torch.bfloat16):
+        q, k, v = make_qkv(1, 4, 512, seed=1, dtype=dtype)
+        for causal in (False, True):
+            o = oracle.emulate_sageattn(q, k, v, is_causal=causal)["o"].double()
+            ex = oracle.exact_attention(q, k, v, is_causal=causal)
+            rel = ((o - ex).pow(2).mean().sqrt() / ex.pow(2).mean().sqrt()).item()
+            assert rel < 0.08, (dtype, causal, rel)
+
+
+def test_planted_mask_mistake_is_caught():
+    # "key >= row" instead of "key > row" masks the diagonal: the closed form of row 0 fails.
+    q, k, v = make_qkv(1, 1, 64, seed=8)
+    r = oracle.emulate_sageattn(q, k, v, is_causal=True)
+    s = r["c_q"][0, 0] * r["sk"][0, 0] * float((r["q8"][0, 0].float() @ r["k8"][0, 0].float()))
+    assert torch.isfinite(s)
+    # with the mistake every key of row 0 is masked, l = 0 and the output row is all zeros
+    assert r["o"][0, 0, 0].abs().sum() > 0
+
+
+def test_nhd_layout_is_a_view():
+    q, k, v = make_qkv(2, 3, 100, seed=1)
+    a = oracle.emulate_sageattn(q, k, v, is_causal=True)["o"]
+    qn, kn, vn = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    b = oracle.emulate_sageattn(qn, kn, vn, tensor_layout="NHD", is_causal=True)["o"]
+    assert torch.equal(b.transpose(1, 2), a)
