@@ -2,7 +2,7 @@
 //
 // Scheme (the reference's, kernels/hip/sk1_t6i.hip:84-299 and sk1_t4a1s.hip): Q is quantized per
 // row inside the kernel (int8 for fp16 inputs, e4m3 for bf16), K8/SK/V8T/SV'/S come from the
-// prologue. Per 64-key block: scores s = fp32(Q8.K8) * (c_q * SK), one running-max update, p =
+// prologue. Per 64-key block: scores s = c_q * SK * (Q8.K8), one running-max update, p =
 // exp2(s - m), l += sum p, p8 = e4m3(p * SV' * 448), acc = acc * alpha + p8 . V8; the epilogue
 // writes acc * S / (l * 448).
 //
@@ -16,9 +16,18 @@
 // * The K rows fed to the S^T MFMA are permuted so that lane half h receives keys 32h .. 32h+31 of
 //   the block in register order; V8T's 32 contiguous bytes per (d, h) are then exactly the V^T
 //   operand. (Which K row occupies which MFMA row is free: the reduction is over d.)
-// * K/V tiles are double-buffered in LDS with one barrier per block; the next block's global loads
-//   are in flight during the current block's MFMAs. K rows use an XOR swizzle on 16-byte chunks,
-//   V^T rows a 16-byte pad, so every MFMA operand read is bank-conflict free.
+// * The softmax is the VALU bottleneck (the MFMA work per score is 256 MACs = 1/16 clock per CU;
+//   the VALU runs 64 lanes per clock per CU), so it is written for the fewest VALU instructions per
+//   score: the int8 accumulator is seeded with the bit pattern of 1.5 * 2^23, which makes its
+//   result the float 1.5*2^23 + (Q8.K8) exactly, so ONE fma with (SK, -RN(1.5*2^23*SK)) gives
+//   x = (Q8.K8)*SK (to within one integer unit of the dot product); the running max is kept in
+//   x units per query, so the exp2 argument c_q*x - c_q*m is ONE more fma. Per score: fma, max3/2,
+//   fma, exp2, add, mul, cvt_pk/2.
+// * Software pipeline: the S^T MFMAs of block j+1 are issued before the softmax of block j, and
+//   the P.V MFMAs of block j retire under the next block's softmax.
+// * K and V tiles are staged global -> registers -> LDS, double-buffered, one
+//   barrier per block; K runs one block ahead of V. K rows use an XOR swizzle of their 16-byte
+//   chunks, V^T rows another, so every MFMA operand read is bank-conflict free.
 // * Causal: blocks past the CTA's diagonal are never visited, a wave skips blocks past its own
 //   diagonal, and masks are applied only on diagonal blocks. The grid is a 1-D list of (plane,
 //   q-tile) pairs, remapped so that each XCD (workgroup id mod 8) runs a contiguous range of
@@ -31,7 +40,15 @@ namespace sage {
 constexpr int BM = 128;    // queries per block
 constexpr int BK = 64;     // keys per main-loop step
 constexpr int AT = 256;    // threads per block
-constexpr int VROW = 80;   // LDS bytes per V^T row (64 keys + 16 pad)
+#ifndef SAGE_ATTN_WAVES
+#define SAGE_ATTN_WAVES 2   // waves per SIMD the register budget is sized for
+#endif
+#ifndef SAGE_ATTN_PIPE
+#define SAGE_ATTN_PIPE 0    // 1: issue the next block's S^T MFMAs before this block's softmax
+#endif
+constexpr int MAGIC_I = 0x4B400000;        // bits of 1.5 * 2^23
+constexpr float MAGIC_F = 12582912.0f;     // 1.5 * 2^23
+
 
 // MFMA row r of score tile t (0/1) reads K row kappa(t, r) of the 64-key block. With the 32x32
 // accumulator layout (row = 8*(reg/4) + 4*(lane/32) + reg%4), lane half h then holds keys
@@ -43,6 +60,8 @@ __device__ __forceinline__ int kappa(int t, int r) {
 __device__ __forceinline__ int kswz(int row) {
   return ((row >> 1) & 1) | ((((row)&1) ^ ((row >> 2) & 1)) << 1) | (((row >> 5) & 1) << 2);
 }
+// XOR swizzle of the 16-byte chunk position within a 64-byte V^T row.
+__device__ __forceinline__ int vswz(int d) { return ((d >> 1) ^ (d >> 3)) & 3; }
 
 // Q fragments of one query row, as the S^T MFMA's B operand wants them.
 //   int8: 4 x 16 bytes, fragment dd = columns 32dd + 16h .. +15
@@ -110,16 +129,71 @@ __device__ __forceinline__ f32x16 mfma_f8(const i32x8 a, const i32x8 b, const f3
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
 }
 
+// Score tile pair of one 64-key block: st[t][reg] holds, for lane (q, h), the raw MFMA result for
+// key 32h + 16t + reg -- int8: the bits of the float 1.5*2^23 + Q8.K8; fp8: the fp32 dot product.
+template <bool QK_INT8>
+__device__ __forceinline__ void qk_block(const u8* __restrict__ kbuf, const QFrag& qf, int krow0,
+                                         int krow1, int ksw0, int ksw1, int hh, f32x16 (&st)[2]) {
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int krow = t ? krow1 : krow0;
+    const int ksw = t ? ksw1 : ksw0;
+    const u8* kb = kbuf + krow * HD;
+    if (QK_INT8) {
+      i32x16 a;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) a[r] = MAGIC_I;
+#pragma unroll
+      for (int dd = 0; dd < 4; ++dd) {
+        const i32x4 kf = *(const i32x4*)(kb + 16 * ((2 * dd + hh) ^ ksw));
+        a = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf.i8[dd], a, 0, 0, 0);
+      }
+      st[t] = __builtin_bit_cast(f32x16, a);
+    } else {
+      f32x16 a;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) a[r] = 0.0f;
+#pragma unroll
+      for (int dd = 0; dd < 2; ++dd) {
+        const int c0 = 4 * dd + 2 * hh;
+        const i32x4 lo = *(const i32x4*)(kb + 16 * (c0 ^ ksw));
+        const i32x4 hi = *(const i32x4*)(kb + 16 * ((c0 + 1) ^ ksw));
+        const i32x8 kf = (i32x8){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        a = mfma_f8(kf, qf.f8[dd], a);
+      }
+      st[t] = a;
+    }
+  }
+}
+
+// Per-key constants of one 64-key block in LDS: SK, the fma addend -RN(1.5*2^23*SK) (0 for the
+// fp8 Q.K form), and RN(SV' * 448).
+struct ScaleTile {
+  float sk[BK];
+  float nsk[BK];
+  float w[BK];
+};
+
+// Both 32-lane halves of a wave exchange values: returns (lower-half value, upper-half value) in
+// every lane, with one v_permlane32_swap (no LDS round trip).
+__device__ __forceinline__ float max_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <typename T, bool QK_INT8, bool CAUSAL>
-__global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_kernel(
+__global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WAVES, SAGE_ATTN_WAVES))) void attn_fwd_kernel(
     const T* __restrict__ Q, const u8* __restrict__ K8, const float* __restrict__ SK,
     const u8* __restrict__ V8T, const float* __restrict__ SV, const float* __restrict__ Sfold,
     T* __restrict__ O, int64_t q_sb, int64_t q_sh, int64_t q_sr, int64_t o_sb, int64_t o_sh,
     int64_t o_sr, int H, int N, int N_pad, int num_qt, int xcd_span, float sm_scale) {
   __shared__ __attribute__((aligned(16))) u8 sK[2][BK * HD];
-  __shared__ __attribute__((aligned(16))) u8 sV[2][HD * VROW];
-  __shared__ __attribute__((aligned(16))) float sSK[2][BK];
-  __shared__ __attribute__((aligned(16))) float sSV[2][BK];
+  __shared__ __attribute__((aligned(16))) u8 sV[2][HD * BK];
+  __shared__ __attribute__((aligned(16))) ScaleTile sS[2];
 
   // ---- which (plane, q-tile) this block runs ----
   int id = blockIdx.x;
@@ -134,113 +208,127 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   const int q0 = qt * BM + w * 32;
   const int qrow = q0 + l32;
 
+  const u8* Kb = K8 + (int64_t)bh * N_pad * HD;
+  const u8* Vb = V8T + (int64_t)bh * HD * N_pad;
+  const float* SKb = SK + (int64_t)bh * N_pad;
+  const float* SVb = SV + (int64_t)bh * N_pad;
+
+  const int n_blocks = N_pad / BK;
+  const int j_end = CAUSAL ? min(n_blocks, (qt * BM + BM - 1) / BK + 1) : n_blocks;
+  const int w_end = CAUSAL ? min(j_end, (q0 + 31) / BK + 1) : j_end;
+
+  // ---- staging: global -> registers -> LDS. Loads are issued at the top of a main-loop step
+  // and written to LDS at its bottom, so their latency hides under the step's compute; nothing
+  // reads the loaded registers in between (a use would make the compiler wait for every global
+  // load in flight: the counter is in order).
+  // K: thread t carries 32 bytes of row t/4 (16-byte chunks c0 = 2(t%4), c0+1), stored at chunk
+  //    positions c ^ kswz(row).  V: thread t carries 32 bytes (keys 32(t%2)..) of V^T row t/2, chunk
+  //    positions c ^ vswz(d).  Scales: threads 0..15 carry SK (and its fma addend), 16..31 carry
+  //    SV' * 448.
+  u32x4 kr0, kr1, vr0, vr1;
+  f32x4 sr;
+  const float* sbase = ((tid & 31) < 16 ? SKb : SVb) + 4 * (tid & 15);
+  const int k_row = tid >> 2, k_c0 = 2 * (tid & 3), k_sw = kswz(tid >> 2);
+  const int v_d = tid >> 1, v_c0 = 2 * (tid & 1), v_sw = vswz(tid >> 1);
+  auto load_k = [&](int j) {
+    const u8* kp = Kb + (int64_t)(BK * j + k_row) * HD + 16 * k_c0;
+    kr0 = *(const u32x4*)kp;
+    kr1 = *(const u32x4*)(kp + 16);
+  };
+  auto load_v = [&](int j) {
+    const u8* vp = Vb + (int64_t)v_d * N_pad + BK * j + 16 * v_c0;
+    vr0 = *(const u32x4*)vp;
+    vr1 = *(const u32x4*)(vp + 16);
+    sr = *(const f32x4*)(sbase + BK * j);
+  };
+  auto store_k = [&](int buf) {
+    *(u32x4*)&sK[buf][k_row * HD + 16 * (k_c0 ^ k_sw)] = kr0;
+    *(u32x4*)&sK[buf][k_row * HD + 16 * ((k_c0 + 1) ^ k_sw)] = kr1;
+  };
+  auto store_v = [&](int buf) {
+    *(u32x4*)&sV[buf][v_d * BK + 16 * (v_c0 ^ v_sw)] = vr0;
+    *(u32x4*)&sV[buf][v_d * BK + 16 * ((v_c0 + 1) ^ v_sw)] = vr1;
+    if (tid < 16) {
+      *(f32x4*)&sS[buf].sk[4 * tid] = sr;
+      f32x4 n;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) n[e] = QK_INT8 ? -(MAGIC_F * sr[e]) : 0.0f;
+      *(f32x4*)&sS[buf].nsk[4 * tid] = n;
+    } else if (tid < 32) {
+      const f32x4 w4 = sr * P_SCALE;
+      *(f32x4*)&sS[buf].w[4 * tid - 64] = w4;
+    }
+  };
+
+  // Start the block-0 loads before the Q quantization so they overlap it.
+  load_k(0);
+  load_v(0);
+
   // ---- Q: per-row quantization straight into MFMA fragments ----
   QFrag qf;
   float sq, cq;
   quant_q_row<T, QK_INT8>(Q + b * q_sb + hd * q_sh + (int64_t)qrow * q_sr, qrow < N, hh, sm_scale,
                           qf, sq, cq);
   (void)sq;
-
-  const u8* Kb = K8 + (int64_t)bh * N_pad * HD;
-  const u8* Vb = V8T + (int64_t)bh * HD * N_pad;
-  const float* SKb = SK + (int64_t)bh * N_pad;
-  const float* SVb = SV + (int64_t)bh * N_pad;
   const float Sb = Sfold[bh];
-
-  const int n_blocks = N_pad / BK;
-  const int j_end = CAUSAL ? min(n_blocks, (qt * BM + BM - 1) / BK + 1) : n_blocks;
-  const int w_end = CAUSAL ? min(j_end, (q0 + 31) / BK + 1) : j_end;
-
-  // ---- staging: global -> registers -> LDS ----
-  u32x4 kr0, kr1, vr0, vr1;
-  f32x4 sr = {0.f, 0.f, 0.f, 0.f};
-  auto gload = [&](int j) {
-    const u8* kp = Kb + (int64_t)(BK * j + (tid >> 2)) * HD + 32 * (tid & 3);
-    kr0 = *(const u32x4*)kp;
-    kr1 = *(const u32x4*)(kp + 16);
-    const u8* vp = Vb + (int64_t)(tid >> 1) * N_pad + BK * j + 32 * (tid & 1);
-    vr0 = *(const u32x4*)vp;
-    vr1 = *(const u32x4*)(vp + 16);
-    if (tid < 16)
-      sr = *(const f32x4*)(SKb + BK * j + 4 * tid);
-    else if (tid < 32)
-      sr = *(const f32x4*)(SVb + BK * j + 4 * (tid - 16)) * P_SCALE;
-  };
-  auto lstore = [&](int s) {
-    const int row = tid >> 2, c0 = 2 * (tid & 3), sw = kswz(row);
-    *(u32x4*)&sK[s][row * HD + 16 * (c0 ^ sw)] = kr0;
-    *(u32x4*)&sK[s][row * HD + 16 * ((c0 + 1) ^ sw)] = kr1;
-    u8* vd = &sV[s][(tid >> 1) * VROW + 32 * (tid & 1)];
-    *(u32x4*)vd = vr0;
-    *(u32x4*)(vd + 16) = vr1;
-    if (tid < 16)
-      *(f32x4*)&sSK[s][4 * tid] = sr;
-    else if (tid < 32)
-      *(f32x4*)&sSV[s][4 * (tid - 16)] = sr;
-  };
 
   f32x16 acc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[dt][r] = 0.0f;
-  float m_i = -INFINITY, l_i = 0.0f;
+  float m_x = -INFINITY;     // running max of x = (Q8.K8)*SK for this lane's query
+  float mc = -INFINITY;      // RN(c_q * m_x), the exp2 shift in use
+  float l_i = 0.0f;
 
-  // MFMA row of this lane in the S^T tiles, and its swizzled K rows.
   const int krow0 = kappa(0, l32), krow1 = kappa(1, l32);
   const int ksw0 = kswz(krow0), ksw1 = kswz(krow1);
+  const int vrow = l32;               // + 32 dt
+  const int vsw = vswz(vrow);         // vswz(32dt + r) == vswz(r)
 
-  gload(0);
-  lstore(0);
+  store_k(0);
+  store_v(0);
+  if (SAGE_ATTN_PIPE && j_end > 1) {
+    load_k(1);
+    store_k(1);
+  }
   __syncthreads();
 
+  f32x16 st[2];
+  if (SAGE_ATTN_PIPE && 0 < w_end) qk_block<QK_INT8>(sK[0], qf, krow0, krow1, ksw0, ksw1, hh, st);
+
   for (int j = 0; j < j_end; ++j) {
-    const int s = j & 1;
-    const bool more = (j + 1 < j_end);
-    if (more) gload(j + 1);
+    const int cur = j & 1, nxt = cur ^ 1;
+    // Loads for the following blocks. Pipelined: K(j+2) goes to the K buffer read last step
+    // (K runs one block ahead of V); otherwise K(j+1). V and the scales of j+1 go to the buffers
+    // read last step.
+    const int kj = SAGE_ATTN_PIPE ? j + 2 : j + 1;
+    if (kj < j_end) load_k(kj);
+    if (j + 1 < j_end) load_v(j + 1);
 
     if (!CAUSAL || j < w_end) {
-      // ---------- S^T = K . Q^T for 64 keys: two 32x32 tiles ----------
-      float sc[32];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int krow = t ? krow1 : krow0;
-        const int ksw = t ? ksw1 : ksw0;
-        const u8* kb = &sK[s][krow * HD];
-        if (QK_INT8) {
-          i32x16 a;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) a[r] = 0;
-#pragma unroll
-          for (int dd = 0; dd < 4; ++dd) {
-            const i32x4 kf = *(const i32x4*)(kb + 16 * ((2 * dd + hh) ^ ksw));
-            a = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf.i8[dd], a, 0, 0, 0);
-          }
-#pragma unroll
-          for (int r = 0; r < 16; ++r) sc[16 * t + r] = (float)a[r];
-        } else {
-          f32x16 a;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) a[r] = 0.0f;
-#pragma unroll
-          for (int dd = 0; dd < 2; ++dd) {
-            const int c0 = 4 * dd + 2 * hh;
-            const i32x4 lo = *(const i32x4*)(kb + 16 * (c0 ^ ksw));
-            const i32x4 hi = *(const i32x4*)(kb + 16 * ((c0 + 1) ^ ksw));
-            const i32x8 kf = (i32x8){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-            a = mfma_f8(kf, qf.f8[dd], a);
-          }
-#pragma unroll
-          for (int r = 0; r < 16; ++r) sc[16 * t + r] = a[r];
-        }
+      f32x16 sn[2];
+      bool have_next = false;
+      if (SAGE_ATTN_PIPE) {
+        // S^T of the next block: its MFMAs retire while this block's softmax runs
+        have_next = (j + 1 < (CAUSAL ? w_end : j_end));
+        if (have_next) qk_block<QK_INT8>(sK[nxt], qf, krow0, krow1, ksw0, ksw1, hh, sn);
+      } else {
+        qk_block<QK_INT8>(sK[cur], qf, krow0, krow1, ksw0, ksw1, hh, st);
       }
-      // ---------- scale, mask, one row max per 64 keys ----------
-      const float* skb = &sSK[s][32 * hh];
+
+      // ---------- x = (Q8.K8) * SK, mask, one row max per 64 keys ----------
+      const ScaleTile& sc = sS[cur];
+      float x[32];
 #pragma unroll
       for (int k4 = 0; k4 < 8; ++k4) {
-        const f32x4 kv = *(const f32x4*)(skb + 4 * k4);
+        const f32x4 kv = *(const f32x4*)&sc.sk[32 * hh + 4 * k4];
+        const f32x4 nv = *(const f32x4*)&sc.nsk[32 * hh + 4 * k4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sc[4 * k4 + e] = sc[4 * k4 + e] * (cq * kv[e]);
+        for (int e = 0; e < 4; ++e) {
+          const int jj = 4 * k4 + e;
+          x[jj] = __builtin_fmaf(st[jj >> 4][jj & 15], kv[e], nv[e]);
+        }
       }
       const bool need_mask = CAUSAL ? (BK * j + BK - 1 > q0) : (BK * j + BK > N);
       if (need_mask) {
@@ -248,35 +336,42 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
           const int key = key0 + i;
-          if (CAUSAL ? (key > qrow) : (key >= N)) sc[i] = -INFINITY;
+          if (CAUSAL ? (key > qrow) : (key >= N)) x[i] = -INFINITY;
         }
       }
-      float lmax = sc[0];
+      // tree max over the lane's 32 scores, then across the two lane halves
+      float g[4];
 #pragma unroll
-      for (int i = 1; i < 32; ++i) lmax = fmaxf(lmax, sc[i]);
-      lmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
-      const float m_new = fmaxf(m_i, lmax);
-      const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_i - m_use);
-      m_i = m_new;
+      for (int k = 0; k < 4; ++k) {
+        const float* y = x + 8 * k;
+        g[k] = fmaxf(fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])),
+                     fmaxf(fmaxf(y[4], y[5]), fmaxf(y[6], y[7])));
+      }
+      const float mx = max_halves(fmaxf(fmaxf(g[0], g[1]), fmaxf(g[2], g[3])));
+      // Exact running max, as the reference keeps it (one update per 64 keys): p8 then rounds
+      // exactly like the reference's. alpha is exp2(0) = 1 exactly when the max did not move.
+      const float m_new = fmaxf(m_x, mx);
+      const float mc_new = cq * ((m_new == -INFINITY) ? 0.0f : m_new);
+      const float alpha = __builtin_amdgcn_exp2f(mc - mc_new);
+      m_x = m_new;
+      mc = mc_new;
 
-      // ---------- P = exp2(s - m), row sum, fold into e4m3 ----------
-      const float* svb = &sSV[s][32 * hh];
-      float psum = 0.0f;
+      // ---------- P = exp2(c_q*x - mc), row sum, fold into e4m3 ----------
+      float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       i32x8 pb;
 #pragma unroll
       for (int k4 = 0; k4 < 8; ++k4) {
-        const f32x4 vv = *(const f32x4*)(svb + 4 * k4);
+        const f32x4 wv = *(const f32x4*)&sc.w[32 * hh + 4 * k4];
         float p[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          p[e] = __builtin_amdgcn_exp2f(sc[4 * k4 + e] - m_use);
-          psum += p[e];
-          p[e] *= vv[e];
+          p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[4 * k4 + e], cq, -mc));
+          ps[e] += p[e];
+          p[e] *= wv[e];
         }
         pb[k4] = (int)fp8x4(p[0], p[1], p[2], p[3]);
       }
-      psum += __shfl_xor(psum, 32, 64);
+      const float psum = sum_halves((ps[0] + ps[1]) + (ps[2] + ps[3]));
       l_i = l_i * alpha + psum;
       if (__any(alpha != 1.0f)) {
 #pragma unroll
@@ -288,15 +383,20 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       // ---------- O^T += V^T . P^T ----------
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const u8* vb = &sV[s][(32 * dt + l32) * VROW + 32 * hh];
-        const i32x4 lo = *(const i32x4*)vb;
-        const i32x4 hi = *(const i32x4*)(vb + 16);
+        const u8* vb = &sV[cur][(32 * dt + vrow) * BK];
+        const i32x4 lo = *(const i32x4*)(vb + 16 * ((2 * hh) ^ vsw));
+        const i32x4 hi = *(const i32x4*)(vb + 16 * ((2 * hh + 1) ^ vsw));
         const i32x8 vf = (i32x8){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
         acc[dt] = mfma_f8(vf, pb, acc[dt]);
       }
+      if (SAGE_ATTN_PIPE && have_next) {
+        st[0] = sn[0];
+        st[1] = sn[1];
+      }
     }
 
-    if (more) lstore(s ^ 1);
+    if (kj < j_end) store_k(SAGE_ATTN_PIPE ? cur : nxt);
+    if (j + 1 < j_end) store_v(nxt);
     __syncthreads();
   }
 

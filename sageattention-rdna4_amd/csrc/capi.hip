@@ -136,6 +136,8 @@ int sage_attn_fwd(int dtype, int qk_int8, int causal, const void* q, int64_t q_s
   if (!k8 || !sk || !v8t || !sv || !s) return fail(SAGE_ERR_INVALID, "an input pointer is NULL");
   if (!aligned16(k8) || !aligned16(v8t) || !aligned16(sk) || !aligned16(sv))
     return fail(SAGE_ERR_INVALID, "ptr_align: quantized inputs must be 16-byte aligned");
+  if (!(sm_scale > 0.0f) || !(sm_scale < 3.0e38f))
+    return fail(SAGE_ERR_INVALID, "sm_scale: must be positive and finite (got %g)", (double)sm_scale);
   sage::AttnArgs a;
   a.dtype = dtype;
   a.qk_int8 = qk_int8 ? 1 : 0;
