@@ -1,0 +1,156 @@
+// Device pieces shared by the 32-query-per-wave main loops (attn_fwd.hip, attn_fwd_v3.hip) and
+// the Q parity entry: tile geometry, operand swizzles, the per-row Q quantizer, MFMA wrappers.
+#pragma once
+#include "sage_device.h"
+
+namespace sage {
+
+constexpr int BM = 128;    // queries per block
+constexpr int BK = 64;     // keys per main-loop step
+constexpr int AT = 256;    // threads per block
+#ifndef SAGE_ATTN_WAVES
+#define SAGE_ATTN_WAVES 2   // waves per SIMD the register budget is sized for
+#endif
+#ifndef SAGE_ATTN_PIPE
+#define SAGE_ATTN_PIPE 0    // 1: issue the next block's S^T MFMAs before this block's softmax
+#endif
+constexpr int MAGIC_I = 0x4B400000;        // bits of 1.5 * 2^23
+constexpr float MAGIC_F = 12582912.0f;     // 1.5 * 2^23
+
+
+// MFMA row r of score tile t (0/1) reads K row kappa(t, r) of the 64-key block. With the 32x32
+// accumulator layout (row = 8*(reg/4) + 4*(lane/32) + reg%4), lane half h then holds keys
+// 32h + 16t + reg.
+__device__ __forceinline__ int kappa(int t, int r) {
+  return 32 * ((r >> 2) & 1) + 16 * t + 4 * (r >> 3) + (r & 3);
+}
+// XOR swizzle of the 16-byte chunk position within a 128-byte K row.
+__device__ __forceinline__ int kswz(int row) {
+  return ((row >> 1) & 1) | ((((row)&1) ^ ((row >> 2) & 1)) << 1) | (((row >> 5) & 1) << 2);
+}
+// XOR swizzle of the 16-byte chunk position within a 64-byte V^T row.
+__device__ __forceinline__ int vswz(int d) { return ((d >> 1) ^ (d >> 3)) & 3; }
+
+// Q fragments of one query row, as the S^T MFMA's B operand wants them.
+//   int8: 4 x 16 bytes, fragment dd = columns 32dd + 16h .. +15
+//   fp8 : 2 x 32 bytes, fragment dd = columns 64dd + 32h .. +31
+struct QFrag {
+  i32x4 i8[4];
+  i32x8 f8[2];
+};
+
+// Column of the c-th 8-element chunk a lane loads (c = 0..7), for lane half h.
+template <bool QK_INT8>
+__device__ __forceinline__ int qcol(int c, int h) {
+  return QK_INT8 ? 32 * (c >> 1) + 16 * h + 8 * (c & 1) : 64 * (c >> 2) + 32 * h + 8 * (c & 3);
+}
+
+// Per-row Q quantization, shared by the main loop and the parity entry point.
+// sk1_t6i.hip:91-117 (int8) and sk1_t4a1s.hip:79-105 (fp8):
+//   amax = max(max_d |q|, 1e-12); qinv = RN(127/amax) (or 448); q8 = clamp(rne(RN(q*qinv)))
+//   (fp8: e4m3(clamp(RN(q*qinv), +-448))); sq = RN(amax/127) (or 448); c_q = RN(RN(sm*log2e)*sq).
+// Lanes q and q+32 hold the two halves of the row and exchange their partial absmax.
+template <typename T, bool QK_INT8>
+__device__ __forceinline__ void quant_q_row(const T* __restrict__ qrow_ptr, bool live, int h,
+                                            float sm_scale, QFrag& qf, float& sq, float& cq) {
+  float x[64];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const u32x4 w = live ? *(const u32x4*)(qrow_ptr + qcol<QK_INT8>(c, h)) : (u32x4){0u, 0u, 0u, 0u};
+    unpack8<T>(w, x + 8 * c);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) amax = fmaxf(amax, fabsf(x[i]));
+  amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+  amax = fmaxf(amax, SCALE_FLOOR);
+  const float top = QK_INT8 ? I8_MAX : P_SCALE;
+  const float qinv = __fdiv_rn(top, amax);
+  sq = __fdiv_rn(amax, top);
+  const float smlog = sm_scale * LOG2E_F;
+  cq = smlog * sq;
+  if (QK_INT8) {
+#pragma unroll
+    for (int dd = 0; dd < 4; ++dd) {
+      const float* y = x + 16 * dd;
+      qf.i8[dd] = (i32x4){(int)i8x4(y[0] * qinv, y[1] * qinv, y[2] * qinv, y[3] * qinv),
+                          (int)i8x4(y[4] * qinv, y[5] * qinv, y[6] * qinv, y[7] * qinv),
+                          (int)i8x4(y[8] * qinv, y[9] * qinv, y[10] * qinv, y[11] * qinv),
+                          (int)i8x4(y[12] * qinv, y[13] * qinv, y[14] * qinv, y[15] * qinv)};
+    }
+  } else {
+#pragma unroll
+    for (int dd = 0; dd < 2; ++dd) {
+      const float* y = x + 32 * dd;
+      float z[32];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) z[i] = fminf(fmaxf(y[i] * qinv, -P_SCALE), P_SCALE);
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        qf.f8[dd][k] = (int)fp8x4(z[4 * k], z[4 * k + 1], z[4 * k + 2], z[4 * k + 3]);
+    }
+  }
+}
+
+__device__ __forceinline__ f32x16 mfma_f8(const i32x8 a, const i32x8 b, const f32x16 c) {
+  // e4m3 x e4m3, unit e8m0 block scales (127 = 2^0).
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+// Score tile pair of one 64-key block: st[t][reg] holds, for lane (q, h), the raw MFMA result for
+// key 32h + 16t + reg -- int8: the bits of the float 1.5*2^23 + Q8.K8; fp8: the fp32 dot product.
+template <bool QK_INT8>
+__device__ __forceinline__ void qk_block(const u8* __restrict__ kbuf, const QFrag& qf, int krow0,
+                                         int krow1, int ksw0, int ksw1, int hh, f32x16 (&st)[2]) {
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int krow = t ? krow1 : krow0;
+    const int ksw = t ? ksw1 : ksw0;
+    const u8* kb = kbuf + krow * HD;
+    if (QK_INT8) {
+      i32x16 a;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) a[r] = MAGIC_I;
+#pragma unroll
+      for (int dd = 0; dd < 4; ++dd) {
+        const i32x4 kf = *(const i32x4*)(kb + 16 * ((2 * dd + hh) ^ ksw));
+        a = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf.i8[dd], a, 0, 0, 0);
+      }
+      st[t] = __builtin_bit_cast(f32x16, a);
+    } else {
+      f32x16 a;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) a[r] = 0.0f;
+#pragma unroll
+      for (int dd = 0; dd < 2; ++dd) {
+        const int c0 = 4 * dd + 2 * hh;
+        const i32x4 lo = *(const i32x4*)(kb + 16 * (c0 ^ ksw));
+        const i32x4 hi = *(const i32x4*)(kb + 16 * ((c0 + 1) ^ ksw));
+        const i32x8 kf = (i32x8){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        a = mfma_f8(kf, qf.f8[dd], a);
+      }
+      st[t] = a;
+    }
+  }
+}
+
+// Per-key constants of one 64-key block in LDS: SK, the fma addend -RN(1.5*2^23*SK) (0 for the
+// fp8 Q.K form), and RN(SV' * 448).
+struct ScaleTile {
+  float sk[BK];
+  float nsk[BK];
+  float w[BK];
+};
+
+// Both 32-lane halves of a wave exchange values: returns (lower-half value, upper-half value) in
+// every lane, with one v_permlane32_swap (no LDS round trip).
+__device__ __forceinline__ float max_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+}  // namespace sage
