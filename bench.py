@@ -120,16 +120,34 @@ def cpu_baseline(wl, q, k, v, budget_s=20.0):
         ops = sum(4.0 * 128 * ((r + 1) if causal else N) for r in range(r0, N))
         return ops, t_emu, t_sdpa
 
-    rows = 64
-    ops, te, ts = run(rows)                      # warm-up and calibration
-    scale = max(1.0, budget_s / max(te + ts, 1e-3) * 0.8)
-    rows = int(min(N, max(64, rows * scale)) // 64 * 64) or 64
+    # Two short runs fix the sample's fixed cost (the plane's prologue) and its cost per query row;
+    # the timed run is then sized to take about `budget_s` seconds of CPU.
+    _, te1, ts1 = run(64)
+    _, te2, ts2 = run(192)
+    per_row = max((te2 + ts2 - te1 - ts1) / 128.0, 1e-6)
+    fixed = max(te1 + ts1 - 64 * per_row, 0.0)
+    rows = int(min(N, max(64.0, (budget_s - fixed) / per_row)) // 64 * 64) or 64
     ops, te, ts = run(rows)
     return dict(value=ops / te / 1e9, unit="GOPS", cores=torch.get_num_threads(), kind="port",
                 sample="plane 0 of %d, last %d query rows of N=%d%s, with that plane's prologue; "
                        "ops %.3e, emulation %.2f s" % (B * H, rows, N, " (causal)" if causal else "",
                                                        ops, te),
                 sdpa_cpu_gops=ops / ts / 1e9, sdpa_cpu_s=ts, host_cpus=os.cpu_count())
+
+
+def copy_calibration(mib, reps):
+    """A plain device-to-device copy of `mib` MiB, `reps` times: each launch reads and writes
+    exactly mib MiB, which calibrates what the HBM counters report per algorithmic byte."""
+    import torch
+    n = mib * (1 << 20)
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_launch": n, "reps": reps}), flush=True)
+    return 0
 
 
 def main():
@@ -140,6 +158,9 @@ def main():
     ap.add_argument("--workload", default="c3c", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="instead of the benchmark, run a plain device copy of this many MiB "
+                         "(the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (every GPU box here has one GPU); "
@@ -147,6 +168,8 @@ def main():
         return 2
 
     import torch
+    if args.copy_mib:
+        return copy_calibration(args.copy_mib, max(args.steps, 1))
     from sageattention import sageattn  # noqa: F401
     from sageattention.sk1_backend import SageLib, sk1_forward
 

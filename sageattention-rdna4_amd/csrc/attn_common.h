@@ -11,9 +11,6 @@ constexpr int AT = 256;    // threads per block
 #ifndef SAGE_ATTN_WAVES
 #define SAGE_ATTN_WAVES 2   // waves per SIMD the register budget is sized for
 #endif
-#ifndef SAGE_ATTN_PIPE
-#define SAGE_ATTN_PIPE 0    // 1: issue the next block's S^T MFMAs before this block's softmax
-#endif
 constexpr int MAGIC_I = 0x4B400000;        // bits of 1.5 * 2^23
 constexpr float MAGIC_F = 12582912.0f;     // 1.5 * 2^23
 
@@ -99,18 +96,18 @@ __device__ __forceinline__ f32x16 mfma_f8(const i32x8 a, const i32x8 b, const f3
 
 // Score tile pair of one 64-key block: st[t][reg] holds, for lane (q, h), the raw MFMA result for
 // key 32h + 16t + reg -- int8: the bits of the float 1.5*2^23 + Q8.K8; fp8: the fp32 dot product.
+// `seed` (int8 form) holds MAGIC_I in every element: the accumulator's starting value.
 template <bool QK_INT8>
 __device__ __forceinline__ void qk_block(const u8* __restrict__ kbuf, const QFrag& qf, int krow0,
-                                         int krow1, int ksw0, int ksw1, int hh, f32x16 (&st)[2]) {
+                                         int krow1, int ksw0, int ksw1, int hh, f32x16 (&st)[2],
+                                         const i32x16& seed) {
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int krow = t ? krow1 : krow0;
     const int ksw = t ? ksw1 : ksw0;
     const u8* kb = kbuf + krow * HD;
     if (QK_INT8) {
-      i32x16 a;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) a[r] = MAGIC_I;
+      i32x16 a = seed;
 #pragma unroll
       for (int dd = 0; dd < 4; ++dd) {
         const i32x4 kf = *(const i32x4*)(kb + 16 * ((2 * dd + hh) ^ ksw));

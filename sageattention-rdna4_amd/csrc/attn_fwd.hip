@@ -23,11 +23,10 @@
 //   x = (Q8.K8)*SK (to within one integer unit of the dot product); the running max is kept in
 //   x units per query, so the exp2 argument c_q*x - c_q*m is ONE more fma. Per score: fma, max3/2,
 //   fma, exp2, add, mul, cvt_pk/2.
-// * Software pipeline: the S^T MFMAs of block j+1 are issued before the softmax of block j, and
-//   the P.V MFMAs of block j retire under the next block's softmax.
-// * K and V tiles are staged global -> registers -> LDS, double-buffered, one
-//   barrier per block; K runs one block ahead of V. K rows use an XOR swizzle of their 16-byte
-//   chunks, V^T rows another, so every MFMA operand read is bank-conflict free.
+// * K, V and the per-key constants of block j+1 are loaded into registers at the top of block j
+//   and written to the other half of the double-buffered LDS at its bottom: one barrier per block.
+//   K rows use an XOR swizzle of their 16-byte chunks, V^T rows another, so the MFMA operand reads
+//   are bank-conflict free.
 // * Causal: blocks past the CTA's diagonal are never visited, a wave skips blocks past its own
 //   diagonal, and masks are applied only on diagonal blocks. The grid is a 1-D list of (plane,
 //   q-tile) pairs, remapped so that each XCD (workgroup id mod 8) runs a contiguous range of
@@ -55,7 +54,9 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
   if (CAUSAL) qt = num_qt - 1 - qt;
   const int b = bh / H, hd = bh - b * H;
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // w is wave-uniform; readfirstlane tells the compiler so, which turns every per-wave decision
+  // (causal block skipping) into a scalar branch rather than an EXEC mask.
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
   const int q0 = qt * BM + w * 32;
   const int qrow = q0 + l32;
@@ -140,35 +141,29 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
 
   store_k(0);
   store_v(0);
-  if (SAGE_ATTN_PIPE && j_end > 1) {
-    load_k(1);
-    store_k(1);
-  }
   __syncthreads();
 
-  f32x16 st[2];
-  if (SAGE_ATTN_PIPE && 0 < w_end) qk_block<QK_INT8>(sK[0], qf, krow0, krow1, ksw0, ksw1, hh, st);
+  // The int8 accumulator seed lives in registers for the whole loop; the empty asm makes it
+  // opaque so the compiler keeps it instead of rebuilding 16 registers every block.
+  i32x16 seed;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) seed[r] = MAGIC_I;
+  if (QK_INT8) asm volatile("" : "+v"(seed));
 
-  for (int j = 0; j < j_end; ++j) {
+  // One 64-key block. STAGE: load block j+1 into registers at the top, store it to the other LDS
+  // buffers at the bottom (false only for the last block, which is peeled off the loop so that
+  // no branch separates the P.V MFMAs from the stores).
+  auto block = [&](const int j, auto stage) {
+    constexpr bool STAGE = decltype(stage)::value;
     const int cur = j & 1, nxt = cur ^ 1;
-    // Loads for the following blocks. Pipelined: K(j+2) goes to the K buffer read last step
-    // (K runs one block ahead of V); otherwise K(j+1). V and the scales of j+1 go to the buffers
-    // read last step.
-    const int kj = SAGE_ATTN_PIPE ? j + 2 : j + 1;
-    if (kj < j_end) load_k(kj);
-    if (j + 1 < j_end) load_v(j + 1);
+    if (STAGE) {
+      load_k(j + 1);
+      load_v(j + 1);
+    }
 
     if (!CAUSAL || j < w_end) {
-      f32x16 sn[2];
-      bool have_next = false;
-      if (SAGE_ATTN_PIPE) {
-        // S^T of the next block: its MFMAs retire while this block's softmax runs
-        have_next = (j + 1 < (CAUSAL ? w_end : j_end));
-        if (have_next) qk_block<QK_INT8>(sK[nxt], qf, krow0, krow1, ksw0, ksw1, hh, sn);
-      } else {
-        qk_block<QK_INT8>(sK[cur], qf, krow0, krow1, ksw0, ksw1, hh, st);
-      }
-
+      f32x16 st[2];
+      qk_block<QK_INT8>(sK[cur], qf, krow0, krow1, ksw0, ksw1, hh, st, seed);
       // ---------- x = (Q8.K8) * SK, mask, one row max per 64 keys ----------
       const ScaleTile& sc = sS[cur];
       float x[32];
@@ -184,12 +179,12 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
       }
       const bool need_mask = CAUSAL ? (BK * j + BK - 1 > q0) : (BK * j + BK > N);
       if (need_mask) {
-        const int key0 = BK * j + 32 * hh;
+        // key = key0 + i is dead when key > qrow (causal) or key >= N (tail): compare the
+        // constant i against one per-lane limit.
+        const int lim = (CAUSAL ? qrow + 1 : N) - (BK * j + 32 * hh);
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          const int key = key0 + i;
-          if (CAUSAL ? (key > qrow) : (key >= N)) x[i] = -INFINITY;
-        }
+        for (int i = 0; i < 32; ++i)
+          if (i >= lim) x[i] = -INFINITY;
       }
       // tree max over the lane's 32 scores, then across the two lane halves
       float g[4];
@@ -204,12 +199,15 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
       // exactly like the reference's. alpha is exp2(0) = 1 exactly when the max did not move.
       const float m_new = fmaxf(m_x, mx);
       const float mc_new = cq * ((m_new == -INFINITY) ? 0.0f : m_new);
-      const float alpha = __builtin_amdgcn_exp2f(mc - mc_new);
+      // When the max did not move alpha must be exactly 1 (the reference's exp2(m - m)), which
+      // also lets the wave skip the accumulator rescale. exp2(mc - mc_new) alone would not give
+      // it: the compiler fuses the product into the subtraction, leaving its rounding error.
+      const float alpha = (m_new != m_x) ? __builtin_amdgcn_exp2f(mc - mc_new) : 1.0f;
       m_x = m_new;
       mc = mc_new;
 
       // ---------- P = exp2(c_q*x - mc), row sum, fold into e4m3 ----------
-      float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float ps[4];
       i32x8 pb;
 #pragma unroll
       for (int k4 = 0; k4 < 8; ++k4) {
@@ -218,7 +216,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[4 * k4 + e], cq, -mc));
-          ps[e] += p[e];
+          ps[e] = k4 ? ps[e] + p[e] : p[e];
           p[e] *= wv[e];
         }
         pb[k4] = (int)fp8x4(p[0], p[1], p[2], p[3]);
@@ -241,16 +239,24 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
         const i32x8 vf = (i32x8){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
         acc[dt] = mfma_f8(vf, pb, acc[dt]);
       }
-      if (SAGE_ATTN_PIPE && have_next) {
-        st[0] = sn[0];
-        st[1] = sn[1];
+      // After the last block acc is only read inside the epilogue's `qrow < N` branch, and the
+      // compiler would otherwise sink these MFMAs into it: under a partial EXEC mask the
+      // inactive lanes' V^T operand rows would drop out of every column. Use acc here, with
+      // the whole wave active.
+      if (!STAGE) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) asm volatile("" ::"v"(acc[dt]));
       }
     }
 
-    if (kj < j_end) store_k(SAGE_ATTN_PIPE ? cur : nxt);
-    if (j + 1 < j_end) store_v(nxt);
+    if (STAGE) {
+      store_k(nxt);
+      store_v(nxt);
+    }
     __syncthreads();
-  }
+  };
+  for (int j = 0; j + 1 < j_end; ++j) block(j, std::true_type{});
+  block(j_end - 1, std::false_type{});
 
   // ---------- epilogue: O = acc * S / (l * 448) ----------
   if (qrow < N) {

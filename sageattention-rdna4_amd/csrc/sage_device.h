@@ -59,7 +59,10 @@ __device__ __forceinline__ uint32_t fp8x2(float a, float b) {
 }
 // Four fp32 -> four e4m3 bytes, memory order a, b, c, d.
 __device__ __forceinline__ uint32_t fp8x4(float a, float b, float c, float d) {
-  int r = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  // The first convert writes the low half-word and keeps the high half of its "old" operand,
+  // which the second convert overwrites, so any value does: passing a's own bits lets the
+  // convert write over a's register instead of a zeroed copy.
+  int r = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __float_as_int(a), false);
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, r, true);
 }
 
