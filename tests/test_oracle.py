@@ -284,14 +284,57 @@ def test_emulation_close_to_exact_attention():
             assert rel < 0.08, (dtype, causal, rel)
 
 
-def test_planted_mask_mistake_is_caught():
-    # "key >= row" instead of "key > row" masks the diagonal: the closed form of row 0 fails.
-    q, k, v = make_qkv(1, 1, 64, seed=8)
-    r = oracle.emulate_sageattn(q, k, v, is_causal=True)
-    s = r["c_q"][0, 0] * r["sk"][0, 0] * float((r["q8"][0, 0].float() @ r["k8"][0, 0].float()))
-    assert torch.isfinite(s)
-    # with the mistake every key of row 0 is masked, l = 0 and the output row is all zeros
-    assert r["o"][0, 0, 0].abs().sum() > 0
+MUTATIONS = {
+    # name: (exact source text in attention_tiles, its planted replacement, causal)
+    "causal_mask_off_by_one": ("(keys > rows) if causal", "(keys >= rows) if causal", True),
+    "tail_mask_off_by_one": ("else (keys >= N)", "else (keys > N)", False),
+    "l_not_rescaled": ("l = l * alpha + p.sum(dim=2)", "l = l + p.sum(dim=2)", True),
+    "acc_not_rescaled": ("acc = acc * alpha[:, :, None] +", "acc = acc +", False),
+    "fold_dropped": ("p8 = (p * sv448[:, None, ks])", "p8 = (p * P_SCALE)", True),
+    "keys_reversed_in_tile": ("torch.matmul(qf, kf[:, ks].transpose(1, 2))",
+                              "torch.matmul(qf, kf[:, ks].flip(1).transpose(1, 2))", False),
+}
+
+
+def _mutated_attention_tiles(old, new):
+    import inspect
+    import oracle.sage_scheme as mod
+    src = inspect.getsource(mod.attention_tiles)
+    assert src.count(old) == 1, old
+    ns = dict(vars(mod))
+    exec(compile(src.replace(old, new), "<planted>", "exec"), ns)
+    return ns["attention_tiles"]
+
+
+@pytest.mark.parametrize("name", sorted(MUTATIONS))
+def test_planted_mistakes_are_caught(name, monkeypatch):
+    # Each plausible slip, planted into a copy of the oracle's attention loop, must make the
+    # brute-force pin fail on at least one row (and the unmutated oracle passes the same check).
+    import oracle.sage_scheme as mod
+    old, new, causal = MUTATIONS[name]
+    N = 130
+    q, k, v = make_qkv(1, 1, N, seed=21, k_offset_std=1.0)
+    v[0, 0, 3, :5] = 900.0                       # S > 1, so a dropped fold changes the output
+
+    def mismatched_rows(fn):
+        monkeypatch.setattr(mod, "attention_tiles", fn)
+        r = mod.emulate_sageattn(q, k, v, is_causal=causal)
+        k8 = r["k8"][0].numpy().astype(np.int32)
+        v8t = r["v8t"][0].float().numpy()
+        q8 = r["q8"][0].numpy().astype(np.int32)
+        out = r["o"][0, 0].float().numpy()
+        bad = 0
+        for row in (0, 1, 64, N - 1):
+            want = _brute_force_row(q8[row], r["c_q"][0, row].item(), k8, r["sk"][0].numpy(), v8t,
+                                    r["svp"][0].numpy(), r["s"][0].item(), row, N, causal, True)
+            want = want.astype(np.float16).astype(np.float32)
+            if not np.allclose(out[row], want, rtol=2e-3, atol=2e-4, equal_nan=False):
+                bad += 1
+        return bad
+
+    original = mod.attention_tiles
+    assert mismatched_rows(original) == 0
+    assert mismatched_rows(_mutated_attention_tiles(old, new)) > 0, name
 
 
 def test_nhd_layout_is_a_view():
