@@ -10,7 +10,8 @@ causal (the reference's `bench/bench_attention.py:140`).
 Prints ONE JSON line. Besides the contract fields it carries
 * `roofline`: the main-loop kernel's achieved TFLOP/s (algorithmic ops per launch / its mean
   launch duration, timed with HIP events on the launch stream inside the timed region) against
-  the int8/fp8 dense MFMA peak;
+  the int8/fp8 dense MFMA peak; `traffic` is its HBM bytes per launch from the committed
+  rocprofv3 FETCH_SIZE/WRITE_SIZE summary for the workload (null when none is committed);
 * `prologue`: the prologue pair's achieved HBM GB/s on its algorithmic bytes;
 * `cpu_baseline`: the CPU emulation of the reference scheme (`oracle/`, a "port") and torch CPU
   SDPA, timed on a bounded sample of the same workload on this host's cores.
@@ -82,6 +83,22 @@ def prologue_bytes(B, H, N, smooth_k=True):
     el = B * H * N * 128 * 2
     q8 = B * H * n_pad * 128
     return (2 if smooth_k else 1) * el + el + 2 * q8 + 4 * B * H * n_pad * 4
+
+
+def profiled_traffic(workload):
+    """HBM bytes per main-loop launch for `workload`, from the committed rocprofv3 summary
+    (FETCH_SIZE and WRITE_SIZE scaled by a plain copy; see profiles/), or None."""
+    import re
+    path = os.path.join(ROOT, "profiles", "attn_fwd_%s_hbm_traffic.md" % workload)
+    if not os.path.exists(path):
+        return None
+    pat = re.compile(r"^traffic_bytes_per_launch\[%s\] = (\d+)$" % re.escape(workload))
+    with open(path) as f:
+        for line in f:
+            m = pat.match(line.strip())
+            if m:
+                return int(m.group(1))
+    return None
 
 
 def cpu_baseline(wl, q, k, v, budget_s=20.0):
@@ -230,7 +247,8 @@ def main():
             "global_batch": B, "seq_len": N, "parallelism": "single-gpu"},
         "roofline": {"bound": "mfma", "achieved": round(attn_tflops, 1), "peak": PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(attn_tflops / PEAK_TOPS, 4),
-                     "traffic": None, "kernel": "attn_fwd_kernel", "ms": round(attn_ms, 4)},
+                     "traffic": profiled_traffic(args.workload), "kernel": "attn_fwd_kernel",
+                     "ms": round(attn_ms, 4)},
         "prologue": {"ms": round(pro_ms, 4), "bytes": pbytes, "achieved_GBps": round(pro_gbps, 1),
                      "peak_GBps": HBM_PEAK_GBPS, "frac": round(pro_gbps / HBM_PEAK_GBPS, 4)},
         "cpu_baseline": cpu,
