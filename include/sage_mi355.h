@@ -61,7 +61,11 @@ size_t sage_kv_prologue_workspace_bytes(int64_t BH, int64_t N);
  *   smooth_k  1: subtract the sequence mean of K first
  *   fold      1: write SV' = SV / S into `sv`; 0: leave SV unfolded (S is written either way)
  *   k, v      logical (B, H, N, 128) views with element strides (k_sb, k_sh, k_sr) / (v_...)
- *   outputs   k8, sk, v8t, sv, s (required); mean (may be NULL; written when smooth_k)
+ *   outputs   k8, sk, v8t, sv, s (required); mean (may be NULL; written when smooth_k);
+ *             kconst (may be NULL): the main loop's per-key constants, (B*H, N_pad/64, 3, 64) fp32:
+ *             for each 64-key block SK, the fma addend -RN(1.5*2^23*SK) (0 when !k_int8) and
+ *             RN(SV'*448) -- a layout of SK and SV' (no reference counterpart: the reference's
+ *             kernel derives them from SK/SV itself, `kernels/hip/sk1_t6i.hip:189-207`, `:249-262`)
  *   workspace at least sage_kv_prologue_workspace_bytes(B*H, N) bytes, 256-byte aligned
  */
 int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int fold,
@@ -69,7 +73,7 @@ int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int fold,
                      const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sr,
                      int64_t B, int64_t H, int64_t N, int64_t N_pad,
                      void* k8, float* sk, void* v8t, float* sv, float* mean, float* s,
-                     void* workspace, size_t workspace_bytes, void* stream);
+                     float* kconst, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * The quantized flash-attention main loop (one launch on `stream`).
@@ -79,15 +83,16 @@ int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int fold,
  * `sk1t6i_attn_fwd_c{0,1}` (`kernels/hip/sk1_t6i.hip:308-316`), `sk1t6in_attn_fwd_c{0,1}`
  * (`kernels/hip/sk1_t6in.hip:323-332`) and `sk1t4a1{sb,nb}_attn_fwd_c{0,1}`
  * (`kernels/hip/sk1_t4a1sb.hip:300-308`). Q is quantized per row inside the kernel (int8 when
- * qk_int8, else fp8 e4m3); `sv` must hold SV' (the folded scales) and `s` the fold S.
+ * qk_int8, else fp8 e4m3). The reference's SK and SV' inputs arrive as `kconst`, the prologue's
+ * per-key constants (SK, -RN(1.5*2^23*SK), RN(SV'*448) per 64-key block, written from the folded
+ * SV'); `s` is the fold S.
  *
  *   q, o   logical (B, H, N, 128) views of `dtype`, element strides (q_sb, q_sh, q_sr) / (o_...)
- *   k8 ... the prologue's outputs for the same B, H, N, N_pad and qk_int8
+ *   k8, kconst, v8t, s   the prologue's outputs for the same B, H, N, N_pad and qk_int8
  */
 int sage_attn_fwd(int dtype, int qk_int8, int causal,
                   const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sr,
-                  const void* k8, const float* sk, const void* v8t, const float* sv,
-                  const float* s,
+                  const void* k8, const float* kconst, const void* v8t, const float* s,
                   void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr,
                   int64_t B, int64_t H, int64_t N, int64_t N_pad, float sm_scale, void* stream);
 

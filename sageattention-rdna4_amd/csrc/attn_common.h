@@ -12,7 +12,7 @@ constexpr int AT = 256;    // threads per block
 #define SAGE_ATTN_WAVES 2   // waves per SIMD the register budget is sized for
 #endif
 constexpr int MAGIC_I = 0x4B400000;        // bits of 1.5 * 2^23
-constexpr float MAGIC_F = 12582912.0f;     // 1.5 * 2^23
+constexpr float MAGIC_F = MAGIC_SEED;      // 1.5 * 2^23
 
 
 // MFMA row r of score tile t (0/1) reads K row kappa(t, r) of the 64-key block. With the 32x32
@@ -89,6 +89,15 @@ __device__ __forceinline__ void quant_q_row(const T* __restrict__ qrow_ptr, bool
   }
 }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
+// 16 bytes per lane, global -> LDS, bypassing registers: lane i of the wave lands at
+// lds_wave_base + 16 * i (the LDS base must be the same for the whole wave).
+__device__ __forceinline__ void g2lds16(const void* src, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)lds_wave_base, 16, 0, 0);
+}
+
 __device__ __forceinline__ f32x16 mfma_f8(const i32x8 a, const i32x8 b, const f32x16 c) {
   // e4m3 x e4m3, unit e8m0 block scales (127 = 2^0).
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
@@ -132,11 +141,19 @@ __device__ __forceinline__ void qk_block(const u8* __restrict__ kbuf, const QFra
 }
 
 // Per-key constants of one 64-key block in LDS: SK, the fma addend -RN(1.5*2^23*SK) (0 for the
-// fp8 Q.K form), and RN(SV' * 448).
+// fp8 Q.K form), and RN(SV' * 448) -- the layout the prologue writes them in (768 bytes/block).
 struct ScaleTile {
   float sk[BK];
   float nsk[BK];
   float w[BK];
+};
+
+// One staging buffer of the main loop: a 64-key block's K tile (64 rows x 128 B, XOR-swizzled
+// 16-byte chunks), V^T tile (128 rows x 64 B, swizzled) and per-key constants.
+struct __attribute__((aligned(16))) StageBuf {
+  u8 k[BK * HD];
+  u8 v[HD * BK];
+  ScaleTile s;
 };
 
 // Both 32-lane halves of a wave exchange values: returns (lower-half value, upper-half value) in

@@ -38,13 +38,17 @@ namespace sage {
 
 template <typename T, bool QK_INT8, bool CAUSAL>
 __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WAVES, SAGE_ATTN_WAVES))) void attn_fwd_kernel(
-    const T* __restrict__ Q, const u8* __restrict__ K8, const float* __restrict__ SK,
-    const u8* __restrict__ V8T, const float* __restrict__ SV, const float* __restrict__ Sfold,
+    const T* __restrict__ Q, const u8* __restrict__ K8, const float* __restrict__ KC,
+    const u8* __restrict__ V8T, const float* __restrict__ Sfold,
     T* __restrict__ O, int64_t q_sb, int64_t q_sh, int64_t q_sr, int64_t o_sb, int64_t o_sh,
     int64_t o_sr, int H, int N, int N_pad, int num_qt, int xcd_span, float sm_scale) {
-  __shared__ __attribute__((aligned(16))) u8 sK[2][BK * HD];
-  __shared__ __attribute__((aligned(16))) u8 sV[2][HD * BK];
-  __shared__ __attribute__((aligned(16))) ScaleTile sS[2];
+  // Three staging buffers (K tile, V^T tile, per-key constants), declared as separate objects:
+  // with the buffer chosen at compile time the compiler can tell a DMA into one buffer from reads
+  // of another, and waits for a DMA only where its own buffer is read. (Its wait bookkeeping
+  // tells apart a handful of DMA targets, so there are three objects, not nine.)
+  __shared__ StageBuf sB0;
+  __shared__ StageBuf sB1;
+  __shared__ StageBuf sB2;
 
   // ---- which (plane, q-tile) this block runs ----
   int id = blockIdx.x;
@@ -63,59 +67,45 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
 
   const u8* Kb = K8 + (int64_t)bh * N_pad * HD;
   const u8* Vb = V8T + (int64_t)bh * HD * N_pad;
-  const float* SKb = SK + (int64_t)bh * N_pad;
-  const float* SVb = SV + (int64_t)bh * N_pad;
+  const float* KCb = KC + (int64_t)bh * N_pad * 3;   // 192 floats per 64-key block
 
   const int n_blocks = N_pad / BK;
   const int j_end = CAUSAL ? min(n_blocks, (qt * BM + BM - 1) / BK + 1) : n_blocks;
   const int w_end = CAUSAL ? min(j_end, (q0 + 31) / BK + 1) : j_end;
 
-  // ---- staging: global -> registers -> LDS. Loads are issued at the top of a main-loop step
-  // and written to LDS at its bottom, so their latency hides under the step's compute; nothing
-  // reads the loaded registers in between (a use would make the compiler wait for every global
-  // load in flight: the counter is in order).
-  // K: thread t carries 32 bytes of row t/4 (16-byte chunks c0 = 2(t%4), c0+1), stored at chunk
-  //    positions c ^ kswz(row).  V: thread t carries 32 bytes (keys 32(t%2)..) of V^T row t/2, chunk
-  //    positions c ^ vswz(d).  Scales: threads 0..15 carry SK (and its fma addend), 16..31 carry
-  //    SV' * 448.
-  u32x4 kr0, kr1, vr0, vr1;
-  f32x4 sr;
-  const float* sbase = ((tid & 31) < 16 ? SKb : SVb) + 4 * (tid & 15);
-  const int k_row = tid >> 2, k_c0 = 2 * (tid & 3), k_sw = kswz(tid >> 2);
-  const int v_d = tid >> 1, v_c0 = 2 * (tid & 1), v_sw = vswz(tid >> 1);
-  auto load_k = [&](int j) {
-    const u8* kp = Kb + (int64_t)(BK * j + k_row) * HD + 16 * k_c0;
-    kr0 = *(const u32x4*)kp;
-    kr1 = *(const u32x4*)(kp + 16);
-  };
-  auto load_v = [&](int j) {
-    const u8* vp = Vb + (int64_t)v_d * N_pad + BK * j + 16 * v_c0;
-    vr0 = *(const u32x4*)vp;
-    vr1 = *(const u32x4*)(vp + 16);
-    sr = *(const f32x4*)(sbase + BK * j);
-  };
-  auto store_k = [&](int buf) {
-    *(u32x4*)&sK[buf][k_row * HD + 16 * (k_c0 ^ k_sw)] = kr0;
-    *(u32x4*)&sK[buf][k_row * HD + 16 * ((k_c0 + 1) ^ k_sw)] = kr1;
-  };
-  auto store_v = [&](int buf) {
-    *(u32x4*)&sV[buf][v_d * BK + 16 * (v_c0 ^ v_sw)] = vr0;
-    *(u32x4*)&sV[buf][v_d * BK + 16 * ((v_c0 + 1) ^ v_sw)] = vr1;
-    if (tid < 16) {
-      *(f32x4*)&sS[buf].sk[4 * tid] = sr;
-      f32x4 n;
+  // ---- staging: global -> LDS directly (global_load_lds, 16 bytes per lane), two blocks ahead
+  // into three LDS buffers. Block j+2 is requested at the top of block j, and the wait at the
+  // bottom of block j covers only block j+1's requests, so a tile has two blocks of compute to
+  // arrive (a plane's K/V exceed an XCD's L2: many requests go to the next cache level). Per block
+  // each wave issues five requests: 2 KB of K, 2 KB of V^T and a 192-byte quarter of the per-key
+  // constants.
+  //   K:   request I = 2w + i carries rows 8I..8I+7; lane l lands at byte 16*l of that KB, i.e.
+  //        row 8I + l/8, chunk slot l%8, which holds logical chunk (l%8) ^ kswz(row).
+  //   V^T: request I carries rows d = 16I..16I+15; lane l -> row 16I + l/4, slot l%4 holding
+  //        logical chunk (l%4) ^ vswz(d).
+  //   KC:  lanes 0..11 of wave w carry bytes 192w .. 192w+191 of the block's 768-byte tile.
+  int k_off[2], v_off[2];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) n[e] = QK_INT8 ? -(MAGIC_F * sr[e]) : 0.0f;
-      *(f32x4*)&sS[buf].nsk[4 * tid] = n;
-    } else if (tid < 32) {
-      const f32x4 w4 = sr * P_SCALE;
-      *(f32x4*)&sS[buf].w[4 * tid - 64] = w4;
-    }
+  for (int i = 0; i < 2; ++i) {
+    const int I = 2 * w + i;
+    const int krow = 8 * I + (lane >> 3), kpos = lane & 7;
+    k_off[i] = krow * HD + 16 * (kpos ^ kswz(krow));
+    const int d = 16 * I + (lane >> 2), vpos = lane & 3;
+    v_off[i] = d * N_pad + 16 * (vpos ^ vswz(d));
+  }
+  auto dma = [&](int j, StageBuf& buf) {
+    const u8* kblk = Kb + (int64_t)BK * j * HD;
+    const u8* vblk = Vb + (int64_t)BK * j;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) g2lds16(kblk + k_off[i], buf.k + 1024 * (2 * w + i));
+#pragma unroll
+    for (int i = 0; i < 2; ++i) g2lds16(vblk + v_off[i], buf.v + 1024 * (2 * w + i));
+    if (lane < 12) g2lds16(KCb + 192 * j + 48 * w + 4 * lane, (u8*)&buf.s + 192 * w);
   };
 
-  // Start the block-0 loads before the Q quantization so they overlap it.
-  load_k(0);
-  load_v(0);
+  // Blocks 0 and 1 are requested before the Q quantization so they overlap it.
+  dma(0, sB0);
+  if (j_end > 1) dma(1, sB1);
 
   // ---- Q: per-row quantization straight into MFMA fragments ----
   QFrag qf;
@@ -139,8 +129,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
   const int vrow = l32;               // + 32 dt
   const int vsw = vswz(vrow);         // vswz(32dt + r) == vswz(r)
 
-  store_k(0);
-  store_v(0);
+  __builtin_amdgcn_s_waitcnt(0);    // blocks 0 and 1 landed (once per block of queries)
   __syncthreads();
 
   // The int8 accumulator seed lives in registers for the whole loop; the empty asm makes it
@@ -150,22 +139,27 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
   for (int r = 0; r < 16; ++r) seed[r] = MAGIC_I;
   if (QK_INT8) asm volatile("" : "+v"(seed));
 
-  // One 64-key block. STAGE: load block j+1 into registers at the top, store it to the other LDS
-  // buffers at the bottom (false only for the last block, which is peeled off the loop so that
-  // no branch separates the P.V MFMAs from the stores).
-  auto block = [&](const int j, auto stage) {
-    constexpr bool STAGE = decltype(stage)::value;
-    const int cur = j & 1, nxt = cur ^ 1;
-    if (STAGE) {
-      load_k(j + 1);
-      load_v(j + 1);
-    }
+  // One 64-key block j, whose tiles are in buffer P = j % 3 (chosen at compile time, so that the
+  // compiler can tell the requests in flight to other buffers from this block's reads). At the
+  // top: request block j+2 into buffer (P+2) % 3, which block j-1 read and every wave has
+  // finished with (barrier). At the bottom: wait until this wave's requests for block j+1 have
+  // landed (five requests per block, in order: vmcnt(5) leaves just block j+2's), then barrier.
+  // The barrier is written as asm with a memory clobber: a workgroup fence would also wait for
+  // block j+2's requests.
+  auto block = [&](const int j, auto par) {
+    constexpr int P = decltype(par)::value;
+    StageBuf& bcur = P == 0 ? sB0 : (P == 1 ? sB1 : sB2);
+    StageBuf& bnew = P == 0 ? sB2 : (P == 1 ? sB0 : sB1);
+    const u8* const kcur = bcur.k;
+    const u8* const vcur = bcur.v;
+    const ScaleTile& sc = bcur.s;
+    const bool more2 = j + 2 < j_end;
+    if (more2) dma(j + 2, bnew);
 
     if (!CAUSAL || j < w_end) {
       f32x16 st[2];
-      qk_block<QK_INT8>(sK[cur], qf, krow0, krow1, ksw0, ksw1, hh, st, seed);
+      qk_block<QK_INT8>(kcur, qf, krow0, krow1, ksw0, ksw1, hh, st, seed);
       // ---------- x = (Q8.K8) * SK, mask, one row max per 64 keys ----------
-      const ScaleTile& sc = sS[cur];
       float x[32];
 #pragma unroll
       for (int k4 = 0; k4 < 8; ++k4) {
@@ -233,30 +227,28 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
       // ---------- O^T += V^T . P^T ----------
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const u8* vb = &sV[cur][(32 * dt + vrow) * BK];
+        const u8* vb = &vcur[(32 * dt + vrow) * BK];
         const i32x4 lo = *(const i32x4*)(vb + 16 * ((2 * hh) ^ vsw));
         const i32x4 hi = *(const i32x4*)(vb + 16 * ((2 * hh + 1) ^ vsw));
         const i32x8 vf = (i32x8){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
         acc[dt] = mfma_f8(vf, pb, acc[dt]);
       }
-      // After the last block acc is only read inside the epilogue's `qrow < N` branch, and the
-      // compiler would otherwise sink these MFMAs into it: under a partial EXEC mask the
-      // inactive lanes' V^T operand rows would drop out of every column. Use acc here, with
-      // the whole wave active.
-      if (!STAGE) {
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) asm volatile("" ::"v"(acc[dt]));
-      }
     }
 
-    if (STAGE) {
-      store_k(nxt);
-      store_v(nxt);
-    }
-    __syncthreads();
+    if (more2)
+      asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   };
-  for (int j = 0; j + 1 < j_end; ++j) block(j, std::true_type{});
-  block(j_end - 1, std::false_type{});
+  for (int j = 0; j < j_end; j += 3) {
+    block(j, std::integral_constant<int, 0>{});
+    if (j + 1 < j_end) block(j + 1, std::integral_constant<int, 1>{});
+    if (j + 2 < j_end) block(j + 2, std::integral_constant<int, 2>{});
+  }
+  // acc is read below only inside the divergent `qrow < N` branch; keep the loop's MFMAs out
+  // of it (an MFMA under a partial EXEC mask loses the inactive lanes' operand rows).
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) asm volatile("" ::"v"(acc[dt]));
 
   // ---------- epilogue: O = acc * S / (l * 448) ----------
   if (qrow < N) {
@@ -352,7 +344,7 @@ static void launch_attn_t(const AttnArgs& a, hipStream_t stream) {
   const int total = num_qt * BH;
   const int span = (total / 8) * 8;
   hipLaunchKernelGGL((attn_fwd_kernel<T, QK_INT8, CAUSAL>), dim3(total), dim3(AT), 0, stream,
-                     (const T*)a.q, (const u8*)a.k8, a.sk, (const u8*)a.v8t, a.sv, a.s, (T*)a.o,
+                     (const T*)a.q, (const u8*)a.k8, a.kconst, (const u8*)a.v8t, a.s, (T*)a.o,
                      a.q_sb, a.q_sh, a.q_sr, a.o_sb, a.o_sh, a.o_sr, (int)a.H, (int)a.N,
                      (int)a.N_pad, num_qt, span, a.sm_scale);
 }

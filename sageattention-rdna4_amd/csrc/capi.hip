@@ -77,8 +77,8 @@ size_t sage_kv_prologue_workspace_bytes(int64_t BH, int64_t N) {
 int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int fold, const void* k, int64_t k_sb,
                      int64_t k_sh, int64_t k_sr, const void* v, int64_t v_sb, int64_t v_sh,
                      int64_t v_sr, int64_t B, int64_t H, int64_t N, int64_t N_pad, void* k8,
-                     float* sk, void* v8t, float* sv, float* mean, float* s, void* workspace,
-                     size_t workspace_bytes, void* stream) {
+                     float* sk, void* v8t, float* sv, float* mean, float* s, float* kconst,
+                     void* workspace, size_t workspace_bytes, void* stream) {
   if (dtype != SAGE_F16 && dtype != SAGE_BF16)
     return fail(SAGE_ERR_INVALID, "dtype: unsupported dtype code %d", dtype);
   if (dtype == SAGE_BF16 && k_int8)
@@ -88,7 +88,7 @@ int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int fold, const void* 
   if ((rc = check_view("k", k, k_sb, k_sh, k_sr))) return rc;
   if ((rc = check_view("v", v, v_sb, v_sh, v_sr))) return rc;
   if (!k8 || !sk || !v8t || !sv || !s) return fail(SAGE_ERR_INVALID, "an output pointer is NULL");
-  if (!aligned16(k8) || !aligned16(v8t) || !aligned16(sk) || !aligned16(sv))
+  if (!aligned16(k8) || !aligned16(v8t) || !aligned16(sk) || !aligned16(sv) || !aligned16(kconst))
     return fail(SAGE_ERR_INVALID, "ptr_align: outputs must be 16-byte aligned");
   const size_t need = sage::prologue_workspace_bytes(B * H, N_pad);
   if (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 255u))
@@ -117,12 +117,13 @@ int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int fold, const void* 
   a.sv = sv;
   a.mean = smooth_k ? mean : nullptr;
   a.s = s;
+  a.kconst = kconst;
   a.workspace = workspace;
   return hip_status(sage::launch_prologue(a, (hipStream_t)stream), "sage_kv_prologue launch");
 }
 
 int sage_attn_fwd(int dtype, int qk_int8, int causal, const void* q, int64_t q_sb, int64_t q_sh,
-                  int64_t q_sr, const void* k8, const float* sk, const void* v8t, const float* sv,
+                  int64_t q_sr, const void* k8, const float* kconst, const void* v8t,
                   const float* s, void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr, int64_t B,
                   int64_t H, int64_t N, int64_t N_pad, float sm_scale, void* stream) {
   if (dtype != SAGE_F16 && dtype != SAGE_BF16)
@@ -133,8 +134,8 @@ int sage_attn_fwd(int dtype, int qk_int8, int causal, const void* q, int64_t q_s
   if (rc) return rc;
   if ((rc = check_view("q", q, q_sb, q_sh, q_sr))) return rc;
   if ((rc = check_view("o", o, o_sb, o_sh, o_sr))) return rc;
-  if (!k8 || !sk || !v8t || !sv || !s) return fail(SAGE_ERR_INVALID, "an input pointer is NULL");
-  if (!aligned16(k8) || !aligned16(v8t) || !aligned16(sk) || !aligned16(sv))
+  if (!k8 || !kconst || !v8t || !s) return fail(SAGE_ERR_INVALID, "an input pointer is NULL");
+  if (!aligned16(k8) || !aligned16(v8t) || !aligned16(kconst))
     return fail(SAGE_ERR_INVALID, "ptr_align: quantized inputs must be 16-byte aligned");
   if (!(sm_scale > 0.0f) || !(sm_scale < 3.0e38f))
     return fail(SAGE_ERR_INVALID, "sm_scale: must be positive and finite (got %g)", (double)sm_scale);
@@ -147,9 +148,8 @@ int sage_attn_fwd(int dtype, int qk_int8, int causal, const void* q, int64_t q_s
   a.q_sh = q_sh;
   a.q_sr = q_sr;
   a.k8 = k8;
-  a.sk = sk;
+  a.kconst = kconst;
   a.v8t = v8t;
-  a.sv = sv;
   a.s = s;
   a.o = o;
   a.o_sb = o_sb;

@@ -176,7 +176,8 @@ template <typename T, bool KINT8>
 __global__ __launch_bounds__(PT) void k_quant_kernel(
     const T* __restrict__ K, u8* __restrict__ K8, float* __restrict__ SK, float* __restrict__ SV,
     const double* __restrict__ part, const float* __restrict__ smax, float* __restrict__ MEAN,
-    float* __restrict__ S_out, int64_t H, int64_t N, int64_t N_pad, int64_t R2, int64_t C1,
+    float* __restrict__ S_out, float* __restrict__ KC, int64_t H, int64_t N, int64_t N_pad,
+    int64_t R2, int64_t C1,
     int64_t k_sb, int64_t k_sh, int64_t k_sr, int smooth_k, int fold) {
   __shared__ float mu_s[HD];
   __shared__ float s_fold;
@@ -250,8 +251,23 @@ __global__ __launch_bounds__(PT) void k_quant_kernel(
           word = (u32x2){fp8x4(x[0], x[1], x[2], x[3]), fp8x4(x[4], x[5], x[6], x[7])};
         }
         *(u32x2*)(K8 + (bh * N_pad + n) * HD + 8 * cg) = word;
-        if (cg == 0) SK[bh * N_pad + n] = live ? sk : 1.0f;
-        if (cg == 1 && fold) SV[bh * N_pad + n] = __fdiv_rn(SV[bh * N_pad + n], S);
+        // The main loop's per-key constants of 64-key block n/64 (KC, optional): SK, the fma
+        // addend -RN(1.5*2^23*SK) (0 for e4m3 K) and RN(SV'*448), 64 floats each.
+        float* kc = KC ? KC + (bh * (N_pad / 64) + n / 64) * 192 + (n & 63) : nullptr;
+        if (cg == 0) {
+          const float ske = live ? sk : 1.0f;
+          SK[bh * N_pad + n] = ske;
+          if (kc) {
+            kc[0] = ske;
+            kc[64] = KINT8 ? -(MAGIC_SEED * ske) : 0.0f;
+          }
+        }
+        if (cg == 1) {
+          const float sv = SV[bh * N_pad + n];
+          const float svp = fold ? __fdiv_rn(sv, S) : sv;
+          if (fold) SV[bh * N_pad + n] = svp;
+          if (kc) kc[128] = svp * P_SCALE;
+        }
       }
     }
   }
@@ -271,11 +287,11 @@ static hipError_t launch_prologue_t(const PrologueArgs& a, hipStream_t stream) {
   if (e != hipSuccess) return e;
   if (a.k_int8)
     hipLaunchKernelGGL((k_quant_kernel<T, true>), dim3((unsigned)g.C2, (unsigned)BH), dim3(PT), 0,
-                       stream, (const T*)a.k, (u8*)a.k8, a.sk, a.sv, part, smax, a.mean, a.s, a.H,
+                       stream, (const T*)a.k, (u8*)a.k8, a.sk, a.sv, part, smax, a.mean, a.s, a.kconst, a.H,
                        a.N, a.N_pad, g.R2, g.C1, a.k_sb, a.k_sh, a.k_sr, a.smooth_k, a.fold);
   else
     hipLaunchKernelGGL((k_quant_kernel<T, false>), dim3((unsigned)g.C2, (unsigned)BH), dim3(PT), 0,
-                       stream, (const T*)a.k, (u8*)a.k8, a.sk, a.sv, part, smax, a.mean, a.s, a.H,
+                       stream, (const T*)a.k, (u8*)a.k8, a.sk, a.sv, part, smax, a.mean, a.s, a.kconst, a.H,
                        a.N, a.N_pad, g.R2, g.C1, a.k_sb, a.k_sh, a.k_sr, a.smooth_k, a.fold);
   return hipGetLastError();
 }

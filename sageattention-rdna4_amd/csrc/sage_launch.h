@@ -30,6 +30,7 @@ struct PrologueArgs {
   float* sv;
   float* mean;
   float* s;
+  float* kconst;   // optional: the main loop's per-key constants (B*H, N_pad/64, 3, 64) fp32
   void* workspace;
 };
 hipError_t launch_prologue(const PrologueArgs& a, hipStream_t stream);
@@ -39,9 +40,8 @@ struct AttnArgs {
   const void* q;
   int64_t q_sb, q_sh, q_sr;
   const void* k8;
-  const float* sk;
+  const float* kconst;
   const void* v8t;
-  const float* sv;
   const float* s;
   void* o;
   int64_t o_sb, o_sh, o_sr;

@@ -179,6 +179,7 @@ def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=
     v8t = torch.empty(BH, D, n_pad, device=dev, dtype=torch.float8_e4m3fn)
     sv = torch.empty(BH, n_pad, device=dev, dtype=torch.float32)
     s = torch.empty(BH, device=dev, dtype=torch.float32)
+    kconst = torch.empty(BH, n_pad // 64, 3, 64, device=dev, dtype=torch.float32)
     ws = torch.empty(lib.workspace_bytes(BH, N), device=dev, dtype=torch.uint8)
     if tensor_layout == "NHD":
         out = torch.empty(B, N, H, D, device=dev, dtype=q.dtype)
@@ -190,10 +191,10 @@ def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=
         if events is not None:
             events[0].record()
         lib.kv_prologue(kk, vv, k8, sk, v8t, sv, s, None, ws, k_int8=qk_int8,
-                        smooth_k=bool(smooth_k), fold=True, n_pad=n_pad)
+                        smooth_k=bool(smooth_k), fold=True, n_pad=n_pad, kconst=kconst)
         if events is not None:
             events[1].record()
-        lib.attn_fwd(qq, k8, sk, v8t, sv, s, oo, qk_int8=qk_int8, causal=bool(is_causal),
+        lib.attn_fwd(qq, k8, kconst, v8t, s, oo, qk_int8=qk_int8, causal=bool(is_causal),
                      sm_scale=sm, n_pad=n_pad)
         if events is not None:
             events[2].record()

@@ -105,9 +105,9 @@ class SageLib:
         L.sage_kv_prologue_workspace_bytes.argtypes = [i64, i64]
         L.sage_kv_prologue.restype = i32
         L.sage_kv_prologue.argtypes = ([i32] * 4 + [vp, i64, i64, i64] * 2 + [i64] * 4
-                                       + [vp] * 7 + [ctypes.c_size_t, vp])
+                                       + [vp] * 8 + [ctypes.c_size_t, vp])
         L.sage_attn_fwd.restype = i32
-        L.sage_attn_fwd.argtypes = ([i32] * 3 + [vp, i64, i64, i64] + [vp] * 5
+        L.sage_attn_fwd.argtypes = ([i32] * 3 + [vp, i64, i64, i64] + [vp] * 4
                                     + [vp, i64, i64, i64] + [i64] * 4 + [f32, vp])
         L.sage_quant_q.restype = i32
         L.sage_quant_q.argtypes = [i32, i32, vp, i64, i64, i64, i64, i64, i64, f32, vp, vp, vp, vp]
@@ -128,25 +128,26 @@ class SageLib:
 
     # ------------------------------------------------------------------ entry points
     def kv_prologue(self, k, v, k8, sk, v8t, sv, s, mean, workspace, *, k_int8, smooth_k, fold,
-                    n_pad):
-        """K/V prologue on logical (B, H, N, D) views `k`, `v` (see `sage_kv_prologue`)."""
+                    n_pad, kconst=None):
+        """K/V prologue on logical (B, H, N, D) views `k`, `v` (see `sage_kv_prologue`).
+        `kconst` (optional) receives the main loop's per-key constants, (B*H, N_pad/64, 3, 64)."""
         B, H, N, _ = (int(x) for x in k.shape)
         rc = self.lib.sage_kv_prologue(
             _dtype_code(k.dtype), int(bool(k_int8)), int(bool(smooth_k)), int(bool(fold)),
             _ptr(k), k.stride(0), k.stride(1), k.stride(2),
             _ptr(v), v.stride(0), v.stride(1), v.stride(2),
             B, H, N, int(n_pad), _ptr(k8), _ptr(sk), _ptr(v8t), _ptr(sv), _ptr(mean), _ptr(s),
-            _ptr(workspace), int(workspace.numel() * workspace.element_size()),
+            _ptr(kconst), _ptr(workspace), int(workspace.numel() * workspace.element_size()),
             ctypes.c_void_p(torch_stream(k.device)))
         self._check(rc, "sage_kv_prologue")
 
-    def attn_fwd(self, q, k8, sk, v8t, sv, s, o, *, qk_int8, causal, sm_scale, n_pad):
+    def attn_fwd(self, q, k8, kconst, v8t, s, o, *, qk_int8, causal, sm_scale, n_pad):
         """Main loop on logical (B, H, N, D) views `q`, `o` (see `sage_attn_fwd`)."""
         B, H, N, _ = (int(x) for x in q.shape)
         rc = self.lib.sage_attn_fwd(
             _dtype_code(q.dtype), int(bool(qk_int8)), int(bool(causal)),
             _ptr(q), q.stride(0), q.stride(1), q.stride(2),
-            _ptr(k8), _ptr(sk), _ptr(v8t), _ptr(sv), _ptr(s),
+            _ptr(k8), _ptr(kconst), _ptr(v8t), _ptr(s),
             _ptr(o), o.stride(0), o.stride(1), o.stride(2),
             B, H, N, int(n_pad), ctypes.c_float(float(sm_scale)),
             ctypes.c_void_p(torch_stream(q.device)))

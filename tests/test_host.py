@@ -50,16 +50,16 @@ def test_library_host_calls_without_a_gpu():
     assert L.workspace_bytes(48, 47520) > 48 * 128 * 8
     assert L.workspace_bytes(1, 1) > 0
     i64 = ctypes.c_int64
-    rc = L.lib.sage_attn_fwd(0, 1, 1, None, 8, 8, 8, None, None, None, None, None, None, 8, 8, 8,
+    rc = L.lib.sage_attn_fwd(0, 1, 1, None, 8, 8, 8, None, None, None, None, None, 8, 8, 8,
                              1, 1, 0, 64, ctypes.c_float(0.1), None)
     assert rc == 1 and b"n_lt_1" in L.lib.sage_last_error()
     rc = L.lib.sage_kv_prologue(1, 1, 1, 1, None, 8, 8, 8, None, 8, 8, 8, 1, 1, 10, 64,
-                                *([None] * 7), 0, None)
+                                *([None] * 8), 0, None)
     assert rc == 1 and b"bf16_int8" in L.lib.sage_last_error()
     rc = L.lib.sage_kv_prologue(0, 1, 1, 1, ctypes.c_void_p(16), 8, 8, 4, ctypes.c_void_p(16),
-                                8, 8, 8, 1, 1, 10, 64, *([None] * 7), 0, None)
+                                8, 8, 8, 1, 1, 10, 64, *([None] * 8), 0, None)
     assert rc == 1 and b"stride_align" in L.lib.sage_last_error()
-    rc = L.lib.sage_attn_fwd(0, 1, 0, ctypes.c_void_p(16), 8, 8, 8, None, None, None, None, None,
+    rc = L.lib.sage_attn_fwd(0, 1, 0, ctypes.c_void_p(16), 8, 8, 8, None, None, None, None,
                              ctypes.c_void_p(16), 8, 8, 8, 1, 1, 100, 96, ctypes.c_float(0.1), None)
     assert rc == 1 and b"n_pad" in L.lib.sage_last_error()
 
