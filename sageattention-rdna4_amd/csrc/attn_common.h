@@ -98,6 +98,26 @@ __device__ __forceinline__ void g2lds16(const void* src, void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)lds_wave_base, 16, 0, 0);
 }
 
+// LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lds_void_t*)p;
+}
+
+// The same moves written as instructions the compiler does not see, for a loop that keeps its own
+// count of them: global address = uniform 64-bit base + per-lane 32-bit offset, LDS destination
+// = uniform lds base + 16 * lane (dwordx4) or + 4 * lane (dword). The compiler then neither waits
+// for them (the caller's s_waitcnt does, before the barrier that publishes the data) nor spends
+// per-lane 64-bit adds on the addresses. Any of its own vector-memory waits stay correct: the
+// counter retires in order, so extra operations in flight only make its waits longer.
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(base), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(voff), "s"(base), "s"(lds) : "memory", "m0");
+}
+
 __device__ __forceinline__ f32x16 mfma_f8(const i32x8 a, const i32x8 b, const f32x16 c) {
   // e4m3 x e4m3, unit e8m0 block scales (127 = 2^0).
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
@@ -146,7 +166,20 @@ struct ScaleTile {
   float sk[BK];
   float nsk[BK];
   float w[BK];
+  float pad[BK];   // landing area of the fourth wave's copy (keeps every wave's request count equal)
 };
+
+// Max of 32 values as 16 three-input maxima (v_max3_f32), a tree of depth 4.
+__device__ __forceinline__ float max32(const float* x) {
+  float m[10];
+#pragma unroll
+  for (int i = 0; i < 10; ++i) m[i] = fmaxf(fmaxf(x[3 * i], x[3 * i + 1]), x[3 * i + 2]);
+  const float n0 = fmaxf(fmaxf(m[0], m[1]), m[2]);
+  const float n1 = fmaxf(fmaxf(m[3], m[4]), m[5]);
+  const float n2 = fmaxf(fmaxf(m[6], m[7]), m[8]);
+  const float n3 = fmaxf(fmaxf(m[9], x[30]), x[31]);
+  return fmaxf(fmaxf(fmaxf(n0, n1), n2), n3);
+}
 
 // One staging buffer of the main loop: a 64-key block's K tile (64 rows x 128 B, XOR-swizzled
 // 16-byte chunks), V^T tile (128 rows x 64 B, swizzled) and per-key constants.

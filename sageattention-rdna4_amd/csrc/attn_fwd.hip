@@ -73,34 +73,38 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
   const int j_end = CAUSAL ? min(n_blocks, (qt * BM + BM - 1) / BK + 1) : n_blocks;
   const int w_end = CAUSAL ? min(j_end, (q0 + 31) / BK + 1) : j_end;
 
-  // ---- staging: global -> LDS directly (global_load_lds, 16 bytes per lane), two blocks ahead
-  // into three LDS buffers. Block j+2 is requested at the top of block j, and the wait at the
-  // bottom of block j covers only block j+1's requests, so a tile has two blocks of compute to
-  // arrive (a plane's K/V exceed an XCD's L2: many requests go to the next cache level). Per block
-  // each wave issues five requests: 2 KB of K, 2 KB of V^T and a 192-byte quarter of the per-key
-  // constants.
-  //   K:   request I = 2w + i carries rows 8I..8I+7; lane l lands at byte 16*l of that KB, i.e.
-  //        row 8I + l/8, chunk slot l%8, which holds logical chunk (l%8) ^ kswz(row).
+  // ---- staging: global -> LDS directly (global_load_lds), two blocks ahead into three LDS
+  // buffers. Block j+2 is requested at the top of block j, and the wait at the bottom of block j
+  // covers only block j+1's requests, so a tile has two blocks of compute to arrive (a plane's K/V
+  // exceed an XCD's L2: many requests go to the next cache level). Per block every wave issues
+  // exactly five requests: 2 KB of K, 2 KB of V^T and 256 bytes of the per-key constants.
+  //   K:   request I = 2w + i (16 B/lane) carries rows 8I..8I+7; lane l lands at byte 16*l of that
+  //        KB, i.e. row 8I + l/8, chunk slot l%8, which holds logical chunk (l%8) ^ kswz(row).
   //   V^T: request I carries rows d = 16I..16I+15; lane l -> row 16I + l/4, slot l%4 holding
   //        logical chunk (l%4) ^ vswz(d).
-  //   KC:  lanes 0..11 of wave w carry bytes 192w .. 192w+191 of the block's 768-byte tile.
-  int k_off[2], v_off[2];
+  //   KC:  waves 0..2 carry floats 64w..64w+63 of the block's 192 (4 B/lane); wave 3 repeats
+  //        wave 0's into the tile's pad.
+  uint32_t k_off[2], v_off[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int I = 2 * w + i;
     const int krow = 8 * I + (lane >> 3), kpos = lane & 7;
-    k_off[i] = krow * HD + 16 * (kpos ^ kswz(krow));
+    k_off[i] = (uint32_t)(krow * HD + 16 * (kpos ^ kswz(krow)));
     const int d = 16 * I + (lane >> 2), vpos = lane & 3;
-    v_off[i] = d * N_pad + 16 * (vpos ^ vswz(d));
+    v_off[i] = (uint32_t)(d * N_pad + 16 * (vpos ^ vswz(d)));
   }
+  const uint32_t c_off = (uint32_t)(4 * (64 * (w == 3 ? 0 : w) + lane));
+  const uint32_t c_dst = (uint32_t)(256 * w);
   auto dma = [&](int j, StageBuf& buf) {
-    const u8* kblk = Kb + (int64_t)BK * j * HD;
-    const u8* vblk = Vb + (int64_t)BK * j;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) g2lds16(kblk + k_off[i], buf.k + 1024 * (2 * w + i));
-#pragma unroll
-    for (int i = 0; i < 2; ++i) g2lds16(vblk + v_off[i], buf.v + 1024 * (2 * w + i));
-    if (lane < 12) g2lds16(KCb + 192 * j + 48 * w + 4 * lane, (u8*)&buf.s + 192 * w);
+    const u8* kblk = Kb + (size_t)(BK * HD) * (uint32_t)j;
+    const u8* vblk = Vb + (size_t)BK * (uint32_t)j;
+    const u8* cblk = (const u8*)KCb + (size_t)(192 * 4) * (uint32_t)j;
+    const uint32_t kl = lds_addr(buf.k) + 2048 * w, vl = lds_addr(buf.v) + 2048 * w;
+    dma16(kblk, k_off[0], kl);
+    dma16(kblk, k_off[1], kl + 1024);
+    dma16(vblk, v_off[0], vl);
+    dma16(vblk, v_off[1], vl + 1024);
+    dma4(cblk, c_off, lds_addr(&buf.s) + c_dst);
   };
 
   // Blocks 0 and 1 are requested before the Q quantization so they overlap it.
@@ -180,15 +184,8 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
         for (int i = 0; i < 32; ++i)
           if (i >= lim) x[i] = -INFINITY;
       }
-      // tree max over the lane's 32 scores, then across the two lane halves
-      float g[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float* y = x + 8 * k;
-        g[k] = fmaxf(fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])),
-                     fmaxf(fmaxf(y[4], y[5]), fmaxf(y[6], y[7])));
-      }
-      const float mx = max_halves(fmaxf(fmaxf(g[0], g[1]), fmaxf(g[2], g[3])));
+      // max over the lane's 32 scores (16 three-input maxima), then across the two lane halves
+      const float mx = max_halves(max32(x));
       // Exact running max, as the reference keeps it (one update per 64 keys): p8 then rounds
       // exactly like the reference's. alpha is exp2(0) = 1 exactly when the max did not move.
       const float m_new = fmaxf(m_x, mx);
