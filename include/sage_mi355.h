@@ -34,6 +34,11 @@ extern "C" {
 #define SAGE_F16 0
 #define SAGE_BF16 1
 
+/* main-loop kernel choice of sage_attn_fwd_ex */
+#define SAGE_KERNEL_AUTO 0  /* by size: the 256-query ping-pong from N = 16384 on, else 128 */
+#define SAGE_KERNEL_Q128 1  /* 128 queries per block of 4 waves */
+#define SAGE_KERNEL_Q256 2  /* 256 queries per block of 8 waves, two groups in ping-pong */
+
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
 int sage_version(void);
 
@@ -95,6 +100,19 @@ int sage_attn_fwd(int dtype, int qk_int8, int causal,
                   const void* k8, const float* kconst, const void* v8t, const float* s,
                   void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr,
                   int64_t B, int64_t H, int64_t N, int64_t N_pad, float sm_scale, void* stream);
+
+/*
+ * sage_attn_fwd with the main-loop kernel chosen by the caller (SAGE_KERNEL_*); sage_attn_fwd is
+ * this with SAGE_KERNEL_AUTO. Both kernels compute the same arithmetic in the same order per
+ * query; only the block shape and schedule differ. No counterpart in the reference (one kernel
+ * per dtype there); for benchmarks and for parity tests that cover both kernels.
+ */
+int sage_attn_fwd_ex(int dtype, int qk_int8, int causal,
+                     const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sr,
+                     const void* k8, const float* kconst, const void* v8t, const float* s,
+                     void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr,
+                     int64_t B, int64_t H, int64_t N, int64_t N_pad, float sm_scale, int kernel,
+                     void* stream);
 
 /*
  * Q quantization exactly as the main loop performs it, written out for parity checks.

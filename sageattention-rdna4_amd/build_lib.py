@@ -31,6 +31,7 @@ COMMON_FLAGS = [
 # (one extra VALU instruction per operand on the softmax's critical path).
 FILE_FLAGS = {
     "attn_fwd.hip": ["-fno-honor-nans"],
+    "attn_fwd_pp.hip": ["-fno-honor-nans"],
 }
 
 

@@ -1,6 +1,9 @@
-// Device pieces shared by the 32-query-per-wave main loops (attn_fwd.hip, attn_fwd_v3.hip) and
-// the Q parity entry: tile geometry, operand swizzles, the per-row Q quantizer, MFMA wrappers.
+// Device pieces shared by the 32-query-per-wave main loops (attn_fwd.hip, attn_fwd_pp.hip) and
+// the Q parity entry: tile geometry, operand swizzles, the per-row Q quantizer, MFMA wrappers,
+// the per-block online softmax.
 #pragma once
+#include <type_traits>
+
 #include "sage_device.h"
 
 namespace sage {
@@ -11,8 +14,6 @@ constexpr int AT = 256;    // threads per block
 #ifndef SAGE_ATTN_WAVES
 #define SAGE_ATTN_WAVES 2   // waves per SIMD the register budget is sized for
 #endif
-constexpr int MAGIC_I = 0x4B400000;        // bits of 1.5 * 2^23
-constexpr float MAGIC_F = MAGIC_SEED;      // 1.5 * 2^23
 
 
 // MFMA row r of score tile t (0/1) reads K row kappa(t, r) of the 64-key block. With the 32x32
@@ -124,19 +125,19 @@ __device__ __forceinline__ f32x16 mfma_f8(const i32x8 a, const i32x8 b, const f3
 }
 
 // Score tile pair of one 64-key block: st[t][reg] holds, for lane (q, h), the raw MFMA result for
-// key 32h + 16t + reg -- int8: the bits of the float 1.5*2^23 + Q8.K8; fp8: the fp32 dot product.
-// `seed` (int8 form) holds MAGIC_I in every element: the accumulator's starting value.
+// key 32h + 16t + reg -- int8: the bits of the int32 Q8.K8; fp8: the fp32 dot product.
 template <bool QK_INT8>
 __device__ __forceinline__ void qk_block(const u8* __restrict__ kbuf, const QFrag& qf, int krow0,
-                                         int krow1, int ksw0, int ksw1, int hh, f32x16 (&st)[2],
-                                         const i32x16& seed) {
+                                         int krow1, int ksw0, int ksw1, int hh, f32x16 (&st)[2]) {
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int krow = t ? krow1 : krow0;
     const int ksw = t ? ksw1 : ksw0;
     const u8* kb = kbuf + krow * HD;
     if (QK_INT8) {
-      i32x16 a = seed;
+      i32x16 a;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) a[r] = 0;
 #pragma unroll
       for (int dd = 0; dd < 4; ++dd) {
         const i32x4 kf = *(const i32x4*)(kb + 16 * ((2 * dd + hh) ^ ksw));
@@ -198,6 +199,125 @@ __device__ __forceinline__ float max_halves(float v) {
 __device__ __forceinline__ float sum_halves(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+
+// Calls f(integral_constant<int, i>) for i = I .. N-1, unrolled (compile-time lane selectors).
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+// Every lane receives lane n of its own 16-lane row (DPP row_newbcast:n). The compiler folds the
+// move into the consuming VALU instruction (v_mul_f32_dpp ... row_newbcast:n).
+template <int N>
+__device__ __forceinline__ float row_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + N, 0xF, 0xF, false));
+}
+
+// Per-key constants of one 64-key block, held as broadcast sources: lane l of half h = l/32
+// holds SK and W of keys 32h + (l & 15) (sk0, w0) and 32h + 16 + (l & 15) (sk1, w1). Both 16-lane
+// rows of a half hold the same values, so score jj of a lane (key 32h + jj) finds its constant in
+// lane jj & 15 of its own row. Four 4-byte LDS reads per block instead of 32 floats per constant
+// per lane.
+struct KeyConsts {
+  float sk0, sk1, w0, w1;
+};
+__device__ __forceinline__ KeyConsts load_key_consts(const ScaleTile& sc, int lane) {
+  const int c = 32 * (lane >> 5) + (lane & 15);
+  return {sc.sk[c], sc.sk[c + 16], sc.w[c], sc.w[c + 16]};
+}
+
+// The online softmax of one 64-key block for this lane's query (sk1_t6i.hip:162-279), in two
+// halves that a pipelined loop can run for different blocks side by side.
+//
+// scores_block: x = fp32(Q8.K8) * SK, written over the raw scores (int8: the int32 dot products;
+// fp8: already fp32); masked keys (causal: key > qrow; non-causal: key >= N) -inf; the running max
+// m_new = max(m, max x); returns the block's shift mc = RN(c_q * m_new) (0 while m_new is -inf)
+// and alpha = exp2(mc_prev - mc), exactly 1 when the max did not move (the reference's
+// exp2(m - m)). A chain of dependent steps: the latency-bound half. q0: the wave's first query.
+struct BlockShift {
+  float mc, alpha;
+};
+template <bool QK_INT8, bool CAUSAL>
+__device__ __forceinline__ BlockShift scores_block(f32x16 (&sx)[2], float sk0, float sk1, int j, int q0,
+                                                   int qrow, int N, int hh, float cq, float& m_x,
+                                                   float& mc) {
+  static_for<0, 32>([&](auto ic) {
+    constexpr int jj = decltype(ic)::value;
+    const float v = sx[jj >> 4][jj & 15];
+    const float d = QK_INT8 ? (float)__float_as_int(v) : v;
+    sx[jj >> 4][jj & 15] = d * row_bcast<jj & 15>(jj < 16 ? sk0 : sk1);
+  });
+  const bool need_mask = CAUSAL ? (BK * j + BK - 1 > q0) : (BK * j + BK > N);
+  if (need_mask) {
+    // key = key0 + i is dead when key > qrow (causal) or key >= N (tail): compare the constant
+    // i against one per-lane limit.
+    const int lim = (CAUSAL ? qrow + 1 : N) - (BK * j + 32 * hh);
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+      if (i >= lim) sx[i >> 4][i & 15] = -INFINITY;
+  }
+  // max over the lane's 32 scores (16 three-input maxima), then across the two lane halves
+  float x[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) x[i] = sx[i >> 4][i & 15];
+  const float mx = max_halves(max32(x));
+  const float m_new = fmaxf(m_x, mx);
+  const float mc_new = cq * ((m_new == -INFINITY) ? 0.0f : m_new);
+  // exp2(mc - mc_new) alone would not give exactly 1 for an unmoved max: the compiler fuses the
+  // product into the subtraction, leaving its rounding error.
+  const float alpha = (m_new != m_x) ? __builtin_amdgcn_exp2f(mc - mc_new) : 1.0f;
+  m_x = m_new;
+  mc = mc_new;
+  return {mc_new, alpha};
+}
+
+// probs_block: p = exp2(c_q*x - mc); l = l*alpha + sum p (the row sum is taken before the fold);
+// P8 = e4m3(p * RN(SV'*448)) into pb; acc *= alpha (skipped when every lane of the wave has
+// alpha == 1). Independent steps: the throughput-bound half. w0/w1: the W broadcast sources.
+__device__ __forceinline__ void probs_block(const f32x16 (&x)[2], float w0, float w1, float cq,
+                                            BlockShift sh, float& l_i, f32x16 (&acc)[4], i32x8& pb) {
+  // W enters through an opaque copy: otherwise its broadcasts are hoisted above the preceding
+  // branch, away from the multiplies they would fold into (one extra move per score).
+  asm volatile("" : "+v"(w0), "+v"(w1));
+  float ps[4];
+  static_for<0, 8>([&](auto k4c) {
+    constexpr int k4 = decltype(k4c)::value;
+    float p[4];
+    static_for<0, 4>([&](auto ec) {
+      constexpr int e = decltype(ec)::value;
+      constexpr int jj = 4 * k4 + e;
+      p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[jj >> 4][jj & 15], cq, -sh.mc));
+      ps[e] = k4 ? ps[e] + p[e] : p[e];
+      p[e] *= row_bcast<jj & 15>(jj < 16 ? w0 : w1);
+    });
+    pb[k4] = (int)fp8x4(p[0], p[1], p[2], p[3]);
+  });
+  // P is complete before the rescale branch (else its products sink past it, apart from the
+  // broadcasts they would fold into)
+  asm volatile("" ::"v"(pb));
+  const float psum = sum_halves((ps[0] + ps[1]) + (ps[2] + ps[3]));
+  l_i = l_i * sh.alpha + psum;
+  if (__any(sh.alpha != 1.0f)) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[dt][r] *= sh.alpha;
+  }
+}
+
+// Both halves for one block, in order.
+template <bool QK_INT8, bool CAUSAL>
+__device__ __forceinline__ void softmax_block(f32x16 (&st)[2], const KeyConsts& kc, int j, int q0,
+                                              int qrow, int N, int hh, float cq, float& m_x,
+                                              float& mc, float& l_i, f32x16 (&acc)[4], i32x8& pb) {
+  const BlockShift sh =
+      scores_block<QK_INT8, CAUSAL>(st, kc.sk0, kc.sk1, j, q0, qrow, N, hh, cq, m_x, mc);
+  probs_block(st, kc.w0, kc.w1, cq, sh, l_i, acc, pb);
 }
 
 }  // namespace sage

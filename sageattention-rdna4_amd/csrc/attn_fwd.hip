@@ -136,13 +136,6 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
   __builtin_amdgcn_s_waitcnt(0);    // blocks 0 and 1 landed (once per block of queries)
   __syncthreads();
 
-  // The int8 accumulator seed lives in registers for the whole loop; the empty asm makes it
-  // opaque so the compiler keeps it instead of rebuilding 16 registers every block.
-  i32x16 seed;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) seed[r] = MAGIC_I;
-  if (QK_INT8) asm volatile("" : "+v"(seed));
-
   // One 64-key block j, whose tiles are in buffer P = j % 3 (chosen at compile time, so that the
   // compiler can tell the requests in flight to other buffers from this block's reads). At the
   // top: request block j+2 into buffer (P+2) % 3, which block j-1 read and every wave has
@@ -161,65 +154,11 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
     if (more2) dma(j + 2, bnew);
 
     if (!CAUSAL || j < w_end) {
+      const KeyConsts kc = load_key_consts(sc, lane);
       f32x16 st[2];
-      qk_block<QK_INT8>(kcur, qf, krow0, krow1, ksw0, ksw1, hh, st, seed);
-      // ---------- x = (Q8.K8) * SK, mask, one row max per 64 keys ----------
-      float x[32];
-#pragma unroll
-      for (int k4 = 0; k4 < 8; ++k4) {
-        const f32x4 kv = *(const f32x4*)&sc.sk[32 * hh + 4 * k4];
-        const f32x4 nv = *(const f32x4*)&sc.nsk[32 * hh + 4 * k4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int jj = 4 * k4 + e;
-          x[jj] = __builtin_fmaf(st[jj >> 4][jj & 15], kv[e], nv[e]);
-        }
-      }
-      const bool need_mask = CAUSAL ? (BK * j + BK - 1 > q0) : (BK * j + BK > N);
-      if (need_mask) {
-        // key = key0 + i is dead when key > qrow (causal) or key >= N (tail): compare the
-        // constant i against one per-lane limit.
-        const int lim = (CAUSAL ? qrow + 1 : N) - (BK * j + 32 * hh);
-#pragma unroll
-        for (int i = 0; i < 32; ++i)
-          if (i >= lim) x[i] = -INFINITY;
-      }
-      // max over the lane's 32 scores (16 three-input maxima), then across the two lane halves
-      const float mx = max_halves(max32(x));
-      // Exact running max, as the reference keeps it (one update per 64 keys): p8 then rounds
-      // exactly like the reference's. alpha is exp2(0) = 1 exactly when the max did not move.
-      const float m_new = fmaxf(m_x, mx);
-      const float mc_new = cq * ((m_new == -INFINITY) ? 0.0f : m_new);
-      // When the max did not move alpha must be exactly 1 (the reference's exp2(m - m)), which
-      // also lets the wave skip the accumulator rescale. exp2(mc - mc_new) alone would not give
-      // it: the compiler fuses the product into the subtraction, leaving its rounding error.
-      const float alpha = (m_new != m_x) ? __builtin_amdgcn_exp2f(mc - mc_new) : 1.0f;
-      m_x = m_new;
-      mc = mc_new;
-
-      // ---------- P = exp2(c_q*x - mc), row sum, fold into e4m3 ----------
-      float ps[4];
+      qk_block<QK_INT8>(kcur, qf, krow0, krow1, ksw0, ksw1, hh, st);
       i32x8 pb;
-#pragma unroll
-      for (int k4 = 0; k4 < 8; ++k4) {
-        const f32x4 wv = *(const f32x4*)&sc.w[32 * hh + 4 * k4];
-        float p[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[4 * k4 + e], cq, -mc));
-          ps[e] = k4 ? ps[e] + p[e] : p[e];
-          p[e] *= wv[e];
-        }
-        pb[k4] = (int)fp8x4(p[0], p[1], p[2], p[3]);
-      }
-      const float psum = sum_halves((ps[0] + ps[1]) + (ps[2] + ps[3]));
-      l_i = l_i * alpha + psum;
-      if (__any(alpha != 1.0f)) {
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
-      }
+      softmax_block<QK_INT8, CAUSAL>(st, kc, j, q0, qrow, N, hh, cq, m_x, mc, l_i, acc, pb);
 
       // ---------- O^T += V^T . P^T ----------
 #pragma unroll

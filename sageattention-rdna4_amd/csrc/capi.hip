@@ -122,10 +122,11 @@ int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int fold, const void* 
   return hip_status(sage::launch_prologue(a, (hipStream_t)stream), "sage_kv_prologue launch");
 }
 
-int sage_attn_fwd(int dtype, int qk_int8, int causal, const void* q, int64_t q_sb, int64_t q_sh,
-                  int64_t q_sr, const void* k8, const float* kconst, const void* v8t,
-                  const float* s, void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr, int64_t B,
-                  int64_t H, int64_t N, int64_t N_pad, float sm_scale, void* stream) {
+int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t q_sb,
+                     int64_t q_sh, int64_t q_sr, const void* k8, const float* kconst,
+                     const void* v8t, const float* s, void* o, int64_t o_sb, int64_t o_sh,
+                     int64_t o_sr, int64_t B, int64_t H, int64_t N, int64_t N_pad, float sm_scale,
+                     int kernel, void* stream) {
   if (dtype != SAGE_F16 && dtype != SAGE_BF16)
     return fail(SAGE_ERR_INVALID, "dtype: unsupported dtype code %d", dtype);
   if (dtype == SAGE_BF16 && qk_int8)
@@ -139,6 +140,8 @@ int sage_attn_fwd(int dtype, int qk_int8, int causal, const void* q, int64_t q_s
     return fail(SAGE_ERR_INVALID, "ptr_align: quantized inputs must be 16-byte aligned");
   if (!(sm_scale > 0.0f) || !(sm_scale < 3.0e38f))
     return fail(SAGE_ERR_INVALID, "sm_scale: must be positive and finite (got %g)", (double)sm_scale);
+  if (kernel != SAGE_KERNEL_AUTO && kernel != SAGE_KERNEL_Q128 && kernel != SAGE_KERNEL_Q256)
+    return fail(SAGE_ERR_INVALID, "kernel: unknown main-loop kernel code %d", kernel);
   sage::AttnArgs a;
   a.dtype = dtype;
   a.qk_int8 = qk_int8 ? 1 : 0;
@@ -160,7 +163,20 @@ int sage_attn_fwd(int dtype, int qk_int8, int causal, const void* q, int64_t q_s
   a.N = N;
   a.N_pad = N_pad;
   a.sm_scale = sm_scale;
-  return hip_status(sage::launch_attn_fwd(a, (hipStream_t)stream), "sage_attn_fwd launch");
+  // The 256-query ping-pong pays off on long sequences; at short ones its larger tiles leave too
+  // few blocks per CU and more causal diagonal work, and the 128-query kernel is as fast or faster.
+  const bool q256 = kernel == SAGE_KERNEL_Q256 || (kernel == SAGE_KERNEL_AUTO && N >= 16384);
+  return hip_status(q256 ? sage::launch_attn_fwd_pp(a, (hipStream_t)stream)
+                         : sage::launch_attn_fwd(a, (hipStream_t)stream),
+                    "sage_attn_fwd launch");
+}
+
+int sage_attn_fwd(int dtype, int qk_int8, int causal, const void* q, int64_t q_sb, int64_t q_sh,
+                  int64_t q_sr, const void* k8, const float* kconst, const void* v8t,
+                  const float* s, void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr, int64_t B,
+                  int64_t H, int64_t N, int64_t N_pad, float sm_scale, void* stream) {
+  return sage_attn_fwd_ex(dtype, qk_int8, causal, q, q_sb, q_sh, q_sr, k8, kconst, v8t, s, o,
+                          o_sb, o_sh, o_sr, B, H, N, N_pad, sm_scale, SAGE_KERNEL_AUTO, stream);
 }
 
 int sage_quant_q(int dtype, int qk_int8, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sr,

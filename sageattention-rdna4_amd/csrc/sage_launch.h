@@ -49,6 +49,8 @@ struct AttnArgs {
   float sm_scale;
 };
 hipError_t launch_attn_fwd(const AttnArgs& a, hipStream_t stream);
+// the two-group ping-pong form of the same main loop (256 queries per block of 8 waves)
+hipError_t launch_attn_fwd_pp(const AttnArgs& a, hipStream_t stream);
 
 struct QuantQArgs {
   int dtype, qk_int8;

@@ -156,8 +156,9 @@ def try_sk1_t1(q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=None, 
 
 
 def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=None,
-                smooth_k=True, int8=None, events=None):
+                smooth_k=True, int8=None, events=None, kernel=0):
     """The served path without the envelope check: allocate, prologue (2 launches), main loop.
+    `kernel` picks the main-loop kernel (0: by size, 1: 128 queries per block, 2: 256).
 
     `events`, when given, is a sequence of three `torch.cuda.Event`s recorded on the launch stream
     before the prologue, between the prologue and the main loop, and after the main loop.
@@ -195,7 +196,7 @@ def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=
         if events is not None:
             events[1].record()
         lib.attn_fwd(qq, k8, kconst, v8t, s, oo, qk_int8=qk_int8, causal=bool(is_causal),
-                     sm_scale=sm, n_pad=n_pad)
+                     sm_scale=sm, n_pad=n_pad, kernel=kernel)
         if events is not None:
             events[2].record()
     return out

@@ -109,6 +109,9 @@ class SageLib:
         L.sage_attn_fwd.restype = i32
         L.sage_attn_fwd.argtypes = ([i32] * 3 + [vp, i64, i64, i64] + [vp] * 4
                                     + [vp, i64, i64, i64] + [i64] * 4 + [f32, vp])
+        L.sage_attn_fwd_ex.restype = i32
+        L.sage_attn_fwd_ex.argtypes = ([i32] * 3 + [vp, i64, i64, i64] + [vp] * 4
+                                       + [vp, i64, i64, i64] + [i64] * 4 + [f32, i32, vp])
         L.sage_quant_q.restype = i32
         L.sage_quant_q.argtypes = [i32, i32, vp, i64, i64, i64, i64, i64, i64, f32, vp, vp, vp, vp]
         L.sage_mfma_layout_probe.restype = i32
@@ -141,15 +144,16 @@ class SageLib:
             ctypes.c_void_p(torch_stream(k.device)))
         self._check(rc, "sage_kv_prologue")
 
-    def attn_fwd(self, q, k8, kconst, v8t, s, o, *, qk_int8, causal, sm_scale, n_pad):
-        """Main loop on logical (B, H, N, D) views `q`, `o` (see `sage_attn_fwd`)."""
+    def attn_fwd(self, q, k8, kconst, v8t, s, o, *, qk_int8, causal, sm_scale, n_pad, kernel=0):
+        """Main loop on logical (B, H, N, D) views `q`, `o` (see `sage_attn_fwd_ex`; `kernel`:
+        0 by size, 1 the 128-query kernel, 2 the 256-query ping-pong)."""
         B, H, N, _ = (int(x) for x in q.shape)
-        rc = self.lib.sage_attn_fwd(
+        rc = self.lib.sage_attn_fwd_ex(
             _dtype_code(q.dtype), int(bool(qk_int8)), int(bool(causal)),
             _ptr(q), q.stride(0), q.stride(1), q.stride(2),
             _ptr(k8), _ptr(kconst), _ptr(v8t), _ptr(s),
             _ptr(o), o.stride(0), o.stride(1), o.stride(2),
-            B, H, N, int(n_pad), ctypes.c_float(float(sm_scale)),
+            B, H, N, int(n_pad), ctypes.c_float(float(sm_scale)), int(kernel),
             ctypes.c_void_p(torch_stream(q.device)))
         self._check(rc, "sage_attn_fwd")
 

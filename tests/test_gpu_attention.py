@@ -188,3 +188,54 @@ def test_head_dim_64_is_refused(dtype):
     q, k, v = (t.cuda() for t in make_qkv(1, 4, 512, seed=7, dtype=dtype, d=64))
     with pytest.raises(ValueError, match="head_dim"):
         _sageattn()(q, k, v, tensor_layout="HND")
+
+
+# ---------------------------------------------------------------------------------------------
+# The two main-loop kernels (128 queries per block, and 256 per block in two ping-pong groups)
+# compute every query with the same instructions in the same order, so they must agree bitwise;
+# the 256-query kernel is also held to the oracle directly, at lengths that exercise its tile
+# edges (256-row tiles, causal diagonals inside a tile, ragged tails) and its staging depth.
+# ---------------------------------------------------------------------------------------------
+def _forward(q, k, v, *, causal, kernel, layout="HND", smooth_k=True):
+    from sageattention.sk1_backend import sk1_forward
+    from sageattention.sk1_backend.sk1_loader import SageLib
+    out = sk1_forward(SageLib.get(), q.cuda(), k.cuda(), v.cuda(), tensor_layout=layout,
+                      is_causal=causal, smooth_k=smooth_k, kernel=kernel)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("N", [1, 63, 65, 192, 255, 256, 257, 511, 700, 1025, 2049])
+def test_q256_kernel_equals_q128_bitwise(N, causal, dtype):
+    q, k, v = make_qkv(1, 3, N, seed=N + 7, dtype=dtype, k_offset_std=2.0, outlier_frac=0.01)
+    o128 = _forward(q, k, v, causal=causal, kernel=1)
+    o256 = _forward(q, k, v, causal=causal, kernel=2)
+    assert torch.equal(o128, o256), (o128 - o256).abs().max().item()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_q256_kernel_matches_emulation(causal, dtype):
+    q, k, v = make_qkv(2, 2, 1337, seed=11, dtype=dtype, k_offset_std=2.0, outlier_frac=0.001)
+    ref = oracle.emulate_sageattn(q, k, v, tensor_layout="HND", is_causal=causal)["o"]
+    out = _forward(q, k, v, causal=causal, kernel=2)
+    assert cosine(out, ref) >= COS_MIN
+    assert rel_l1(out, ref) <= REL_L1_MAX
+
+
+def test_q256_kernel_nhd_equals_hnd_bitwise():
+    q, k, v = make_qkv(2, 3, 777, seed=3, dtype=torch.float16, layout="NHD")
+    o_nhd = _forward(q, k, v, causal=True, kernel=2, layout="NHD")
+    hnd = [t.transpose(1, 2).contiguous() for t in (q, k, v)]
+    o_hnd = _forward(*hnd, causal=True, kernel=2)
+    assert torch.equal(o_nhd.transpose(1, 2), o_hnd)
+
+
+def test_auto_kernel_choice_serves_long_sequences():
+    # N = 16384 takes the 256-query kernel by default; it must equal the 128-query kernel there.
+    q, k, v = make_qkv(1, 1, 16384, seed=21, dtype=torch.float16, k_offset_std=2.0)
+    o_auto = _forward(q, k, v, causal=True, kernel=0)
+    o128 = _forward(q, k, v, causal=True, kernel=1)
+    assert torch.equal(o_auto, o128)

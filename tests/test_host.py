@@ -22,7 +22,8 @@ def _declared_symbols():
 def test_header_declares_the_entry_points():
     syms = _declared_symbols()
     for s in ("sage_version", "sage_last_error", "sage_kv_prologue_workspace_bytes",
-              "sage_kv_prologue", "sage_attn_fwd", "sage_quant_q", "sage_mfma_layout_probe"):
+              "sage_kv_prologue", "sage_attn_fwd", "sage_attn_fwd_ex", "sage_quant_q",
+              "sage_mfma_layout_probe"):
         assert s in syms
 
 
@@ -62,6 +63,11 @@ def test_library_host_calls_without_a_gpu():
     rc = L.lib.sage_attn_fwd(0, 1, 0, ctypes.c_void_p(16), 8, 8, 8, None, None, None, None,
                              ctypes.c_void_p(16), 8, 8, 8, 1, 1, 100, 96, ctypes.c_float(0.1), None)
     assert rc == 1 and b"n_pad" in L.lib.sage_last_error()
+    p16 = ctypes.c_void_p(16)
+    rc = L.lib.sage_attn_fwd_ex(0, 1, 0, p16, 12800, 12800, 128, p16, p16, p16, p16,
+                                p16, 12800, 12800, 128, 1, 1, 100, 128, ctypes.c_float(0.1), 7,
+                                None)
+    assert rc == 1 and b"kernel" in L.lib.sage_last_error()
 
 
 def test_strided_view_reason_rule():
