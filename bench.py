@@ -175,6 +175,9 @@ def main():
     ap.add_argument("--workload", default="c3c", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--kernel", type=int, default=0, choices=(0, 1, 2),
+                    help="main-loop kernel: 0 by size (the library's default), 1 the 128-query "
+                         "kernel, 2 the 256-query ping-pong")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of the benchmark, run a plain device copy of this many MiB "
                          "(the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -197,7 +200,10 @@ def main():
     qd, kd, vd = (t.to(dev) for t in (q, k, v))
     lib = SageLib.get()
     call = lambda ev=None: sk1_forward(lib, qd, kd, vd, tensor_layout=layout, is_causal=causal,
-                                       smooth_k=True, events=ev)
+                                       smooth_k=True, events=ev, kernel=args.kernel)
+    # the library's choice by size (sage_attn_fwd_ex): 256 queries per block from N = 16384 on
+    q256 = args.kernel == 2 or (args.kernel == 0 and N >= 16384)
+    kname = "attn_fwd_pp_kernel" if q256 else "attn_fwd_kernel"
     for _ in range(args.warmup):
         call()
     torch.cuda.synchronize()
@@ -247,7 +253,7 @@ def main():
             "global_batch": B, "seq_len": N, "parallelism": "single-gpu"},
         "roofline": {"bound": "mfma", "achieved": round(attn_tflops, 1), "peak": PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(attn_tflops / PEAK_TOPS, 4),
-                     "traffic": profiled_traffic(args.workload), "kernel": "attn_fwd_kernel",
+                     "traffic": profiled_traffic(args.workload), "kernel": kname,
                      "ms": round(attn_ms, 4)},
         "prologue": {"ms": round(pro_ms, 4), "bytes": pbytes, "achieved_GBps": round(pro_gbps, 1),
                      "peak_GBps": HBM_PEAK_GBPS, "frac": round(pro_gbps / HBM_PEAK_GBPS, 4)},
