@@ -276,9 +276,20 @@ __device__ __forceinline__ BlockShift scores_block(f32x16 (&sx)[2], float sk0, f
   return {mc_new, alpha};
 }
 
+// O *= alpha before the block's P.V, skipped when every lane of the wave has alpha == 1.
+__device__ __forceinline__ void rescale_acc(f32x16 (&acc)[4], float alpha) {
+  if (__any(alpha != 1.0f)) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+  }
+}
+
 // probs_block: p = exp2(c_q*x - mc); l = l*alpha + sum p (the row sum is taken before the fold);
-// P8 = e4m3(p * RN(SV'*448)) into pb; acc *= alpha (skipped when every lane of the wave has
-// alpha == 1). Independent steps: the throughput-bound half. w0/w1: the W broadcast sources.
+// P8 = e4m3(p * RN(SV'*448)) into pb; with RESCALE, acc *= alpha (else the caller does it before
+// the block's P.V). Independent steps: the throughput-bound half. w0/w1: the W broadcast sources.
+template <bool RESCALE = true>
 __device__ __forceinline__ void probs_block(const f32x16 (&x)[2], float w0, float w1, float cq,
                                             BlockShift sh, float& l_i, f32x16 (&acc)[4], i32x8& pb) {
   // W enters through an opaque copy: otherwise its broadcasts are hoisted above the preceding
@@ -302,12 +313,7 @@ __device__ __forceinline__ void probs_block(const f32x16 (&x)[2], float w0, floa
   asm volatile("" ::"v"(pb));
   const float psum = sum_halves((ps[0] + ps[1]) + (ps[2] + ps[3]));
   l_i = l_i * sh.alpha + psum;
-  if (__any(sh.alpha != 1.0f)) {
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[dt][r] *= sh.alpha;
-  }
+  if (RESCALE) rescale_acc(acc, sh.alpha);
 }
 
 // Both halves for one block, in order.

@@ -123,8 +123,10 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
     constexpr int P = decltype(par)::value;
     qk_block<QK_INT8>(sB[P].k, qf, krow0, krow1, ksw0, ksw1, hh, st);
   };
+  float alpha_pend = 1.0f;      // alpha of the block whose P.V comes next
   auto pv = [&](auto par) {
     constexpr int P = decltype(par)::value;
+    rescale_acc(acc, alpha_pend);
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       const u8* vb = &sB[P].v[(32 * dt + vrow) * BK];
@@ -147,8 +149,16 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
   // the wave's MFMA phase); the P.V of block j-1 has already been issued
   KeyConsts kcp;
   auto prefetch_consts = [&](auto buf) { kcp = load_key_consts(sB[decltype(buf)::value].s, lane); };
+  // The accumulator rescale by alpha is left to the wave's MFMA phase (rescale_pv): a rescale in
+  // the softmax phase would hold up all 8 waves at the phase's barrier whenever any one of the 4
+  // softmax waves needs it. The softmax phase runs at raised issue priority.
   auto softmax = [&](const int j) {
-    softmax_block<QK_INT8, CAUSAL>(st, kcp, j, q0, qrow, N, hh, cq, m_x, mc, l_i, acc, pb);
+    __builtin_amdgcn_s_setprio(1);
+    const BlockShift sh =
+        scores_block<QK_INT8, CAUSAL>(st, kcp.sk0, kcp.sk1, j, q0, qrow, N, hh, cq, m_x, mc);
+    probs_block<false>(st, kcp.w0, kcp.w1, cq, sh, l_i, acc, pb);
+    alpha_pend = sh.alpha;
+    __builtin_amdgcn_s_setprio(0);
   };
   // A phase's products are pinned before its barrier: without the pins the compiler is free to
   // sink MFMAs (which touch no memory) past the barrier into the next phase.
