@@ -160,7 +160,7 @@ def quant_q(q, sm_scale, int8=True):
 
 
 def attention_tiles(q8, c_q, k8, sk, v8t, svp, s_fold, N, causal, out_dtype, tile=BN,
-                    q_chunk=2048, row0=0):
+                    q_chunk=2048, row0=0, lse_out=None):
     """The main loop's online softmax over key tiles, in the reference's phase order.
 
     Follows `kernels/hip/sk1_t6i.hip:162-299` (and the identical fp8 form of `sk1_t4a1s.hip`):
@@ -179,6 +179,10 @@ def attention_tiles(q8, c_q, k8, sk, v8t, svp, s_fold, N, causal, out_dtype, til
 
     Shapes: q8 (BH, N, D); c_q (BH, N); k8 (BH, n_pad, D); sk, svp (BH, n_pad); v8t (BH, D, n_pad);
     s_fold (BH,). Returns O (BH, N, D) in `out_dtype`.
+
+    `lse_out` ((BH, N) fp32, optional) receives each row's log2-domain sum `m_use + log2(l)` of
+    the final tile (the quantized scores' logsumexp in exp2 units, before any smooth_k
+    correction; `row_lse` turns it into the natural-log value `sageattn` returns).
     """
     BH, NQ, D = q8.shape
     n_pad = k8.shape[1]
@@ -215,7 +219,24 @@ def attention_tiles(q8, c_q, k8, sk, v8t, svp, s_fold, N, causal, out_dtype, til
             m = m_new
         inv = torch.where(l > 0, s_fold[:, None] / (l * P_SCALE), torch.zeros_like(l))
         out[:, r0:r1] = (acc * inv[:, :, None]).to(out_dtype)
+        if lse_out is not None:
+            m_use = torch.where(m == -math.inf, torch.zeros_like(m), m)
+            lse_out[:, r0:r1] = m_use + torch.log2(l)
     return out
+
+
+def row_lse(lse2, q, mean, sm_scale):
+    """The natural-log logsumexp `sageattn(..., return_lse=True)` returns
+    (`sageattention/core.py:1437-1439` of the reference): `lse2 / 1.44269504`, plus
+    `sm_scale * (q . mean)` per row when the keys were smoothed (`mean` not None; `core.py:1401-1403`
+    computes the same correction as `q @ km^T`). lse2 (BH, N) fp32 from `attention_tiles`; q the
+    caller's (BH, N, D) values; mean (BH, D) fp32 or None. Returns (BH, N) fp32.
+    """
+    lse = lse2 / torch.tensor(1.44269504, dtype=torch.float32)
+    if mean is not None:
+        corr = torch.matmul(q.to(torch.float32), mean[:, :, None]).squeeze(-1)
+        lse = lse + corr * torch.tensor(sm_scale, dtype=torch.float32)
+    return lse
 
 
 def emulate_sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=None, smooth_k=True,
@@ -226,8 +247,9 @@ def emulate_sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=Non
     (`sk1_t6i`), bf16 inputs use fp8 Q.K (`sk1_t4a1sb`); `qk_int8=False` forces the fp8 form for
     fp16 inputs. `sm_scale` defaults to `D ** -0.5` (`__init__.py:1165`).
 
-    Returns a dict with `mean, k8, sk, v8t, sv, s, svp, q8, sq, c_q, o` where `o` has the caller's
-    layout and dtype and every other tensor is per (b, h) plane, (BH, ...).
+    Returns a dict with `mean, k8, sk, v8t, sv, s, svp, q8, sq, c_q, o, lse` where `o` has the
+    caller's layout and dtype, `lse` is (B, H, N) fp32 (the `return_lse` output) and every other
+    tensor is per (b, h) plane, (BH, ...).
     """
     qq, kk, vv = (to_hnd(t, tensor_layout) for t in (q, k, v))
     B, H, N, D = qq.shape
@@ -242,12 +264,32 @@ def emulate_sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=Non
     v8t, sv = quant_v(vr, n_pad)
     s, svp = fold_v_scale(sv)
     q8, sq, c_q = quant_q(qr, sm, int8=qk_int8)
-    o = attention_tiles(q8, c_q, k8, sk, v8t, svp, s, N, is_causal, q.dtype)
+    lse2 = torch.empty(BH, N, dtype=torch.float32)
+    o = attention_tiles(q8, c_q, k8, sk, v8t, svp, s, N, is_causal, q.dtype, lse_out=lse2)
     o = o.view(B, H, N, D)
     if tensor_layout == "NHD":
         o = o.transpose(1, 2).contiguous()
+    lse = row_lse(lse2, qr, mean, sm).view(B, H, N)
     return dict(mean=mean, k8=k8, sk=sk, v8t=v8t, sv=sv, s=s, svp=svp, q8=q8, sq=sq, c_q=c_q, o=o,
-                n_pad=n_pad, sm_scale=sm)
+                lse=lse, n_pad=n_pad, sm_scale=sm)
+
+
+def exact_lse(q, k, is_causal=False, sm_scale=None, tensor_layout="HND", q_chunk=1024):
+    """The natural-log logsumexp of each row of Q.K^T * sm_scale, unquantized, in fp64 (the
+    yardstick for `return_lse`; the reference's `_attention_lse_reference`, `core.py:424-467`).
+    Returns (B, H, N) fp64."""
+    qq, kk = (to_hnd(t, tensor_layout).to(torch.float64) for t in (q, k))
+    B, H, N, D = qq.shape
+    sm = float(sm_scale if sm_scale is not None else D ** -0.5)
+    out = torch.empty(B, H, N, dtype=torch.float64)
+    for r0 in range(0, N, q_chunk):
+        r1 = min(N, r0 + q_chunk)
+        s = torch.matmul(qq[:, :, r0:r1], kk.transpose(2, 3)) * sm
+        if is_causal:
+            dead = torch.arange(N)[None, :] > torch.arange(r0, r1)[:, None]
+            s = s.masked_fill(dead, -math.inf)
+        out[:, :, r0:r1] = torch.logsumexp(s, dim=-1)
+    return out
 
 
 def exact_attention(q, k, v, is_causal=False, sm_scale=None, tensor_layout="HND", q_chunk=1024):

@@ -48,14 +48,31 @@ __device__ __forceinline__ int qcol(int c, int h) {
 //   amax = max(max_d |q|, 1e-12); qinv = RN(127/amax) (or 448); q8 = clamp(rne(RN(q*qinv)))
 //   (fp8: e4m3(clamp(RN(q*qinv), +-448))); sq = RN(amax/127) (or 448); c_q = RN(RN(sm*log2e)*sq).
 // Lanes q and q+32 hold the two halves of the row and exchange their partial absmax.
+// With `mu` (the plane's smooth_k mean, 128 fp32), also returns q . mu over the whole row in
+// `qmu` (fp32 products and sums, both lanes get it): the row's logsumexp correction for smooth_k.
 template <typename T, bool QK_INT8>
 __device__ __forceinline__ void quant_q_row(const T* __restrict__ qrow_ptr, bool live, int h,
-                                            float sm_scale, QFrag& qf, float& sq, float& cq) {
+                                            float sm_scale, QFrag& qf, float& sq, float& cq,
+                                            const float* __restrict__ mu = nullptr,
+                                            float* qmu = nullptr) {
   float x[64];
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
     const u32x4 w = live ? *(const u32x4*)(qrow_ptr + qcol<QK_INT8>(c, h)) : (u32x4){0u, 0u, 0u, 0u};
     unpack8<T>(w, x + 8 * c);
+  }
+  if (mu) {
+    float d = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const f32x4 m0 = *(const f32x4*)(mu + qcol<QK_INT8>(c, h));
+      const f32x4 m1 = *(const f32x4*)(mu + qcol<QK_INT8>(c, h) + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) d = __builtin_fmaf(x[8 * c + e], m0[e], d);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) d = __builtin_fmaf(x[8 * c + 4 + e], m1[e], d);
+    }
+    *qmu = d + __shfl_xor(d, 32, 64);
   }
   float amax = 0.0f;
 #pragma unroll
@@ -267,9 +284,12 @@ __device__ __forceinline__ BlockShift scores_block(f32x16 (&sx)[2], float sk0, f
   for (int i = 0; i < 32; ++i) x[i] = sx[i >> 4][i & 15];
   const float mx = max_halves(max32(x));
   const float m_new = fmaxf(m_x, mx);
-  const float mc_new = cq * ((m_new == -INFINITY) ? 0.0f : m_new);
-  // exp2(mc - mc_new) alone would not give exactly 1 for an unmoved max: the compiler fuses the
-  // product into the subtraction, leaving its rounding error.
+  float mc_new = cq * ((m_new == -INFINITY) ? 0.0f : m_new);
+  // mc_new is rounded before it is used: the opaque copy keeps the compiler from fusing the
+  // product into the subtraction below, which it would do or not depending on the surrounding
+  // code (so two kernels would round alpha differently). exp2(mc - mc_new) of the rounded shifts
+  // is then exactly 1 for an unmoved max; the select skips the exp2 there.
+  asm volatile("" : "+v"(mc_new));
   const float alpha = (m_new != m_x) ? __builtin_amdgcn_exp2f(mc - mc_new) : 1.0f;
   m_x = m_new;
   mc = mc_new;
@@ -312,7 +332,7 @@ __device__ __forceinline__ void probs_block(const f32x16 (&x)[2], float w0, floa
   // broadcasts they would fold into)
   asm volatile("" ::"v"(pb));
   const float psum = sum_halves((ps[0] + ps[1]) + (ps[2] + ps[3]));
-  l_i = l_i * sh.alpha + psum;
+  l_i = __builtin_fmaf(l_i, sh.alpha, psum);
   if (RESCALE) rescale_acc(acc, sh.alpha);
 }
 
@@ -324,6 +344,15 @@ __device__ __forceinline__ void softmax_block(f32x16 (&st)[2], const KeyConsts& 
   const BlockShift sh =
       scores_block<QK_INT8, CAUSAL>(st, kc.sk0, kc.sk1, j, q0, qrow, N, hh, cq, m_x, mc);
   probs_block(st, kc.w0, kc.w1, cq, sh, l_i, acc, pb);
+}
+
+
+// The row's natural-log logsumexp of its scores times sm_scale, as the reference returns it
+// (core.py:1437-1439): log2-domain sum RN(c_q*m) + log2(l), divided by 1.44269504, plus
+// sm_scale * (q . mu) when the keys were smoothed.
+__device__ __forceinline__ float row_lse(float mc, float l_i, float sm_scale, float qmu) {
+  const float lse2 = mc + __builtin_amdgcn_logf(l_i);
+  return __builtin_fmaf(sm_scale, qmu, __fdiv_rn(lse2, 1.44269504f));
 }
 
 }  // namespace sage

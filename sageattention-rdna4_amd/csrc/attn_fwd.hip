@@ -41,7 +41,8 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
     const T* __restrict__ Q, const u8* __restrict__ K8, const float* __restrict__ KC,
     const u8* __restrict__ V8T, const float* __restrict__ Sfold,
     T* __restrict__ O, int64_t q_sb, int64_t q_sh, int64_t q_sr, int64_t o_sb, int64_t o_sh,
-    int64_t o_sr, int H, int N, int N_pad, int num_qt, int xcd_span, float sm_scale) {
+    int64_t o_sr, int H, int N, int N_pad, int num_qt, int xcd_span, float sm_scale,
+    float* __restrict__ LSE, const float* __restrict__ KMEAN) {
   // Three staging buffers (K tile, V^T tile, per-key constants), declared as separate objects:
   // with the buffer chosen at compile time the compiler can tell a DMA into one buffer from reads
   // of another, and waits for a DMA only where its own buffer is read. (Its wait bookkeeping
@@ -114,8 +115,9 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
   // ---- Q: per-row quantization straight into MFMA fragments ----
   QFrag qf;
   float sq, cq;
+  float qmu = 0.0f;   // q . mu for the logsumexp's smooth_k correction (when asked)
   quant_q_row<T, QK_INT8>(Q + b * q_sb + hd * q_sh + (int64_t)qrow * q_sr, qrow < N, hh, sm_scale,
-                          qf, sq, cq);
+                          qf, sq, cq, (LSE && KMEAN) ? KMEAN + (int64_t)bh * HD : nullptr, &qmu);
   (void)sq;
   const float Sb = Sfold[bh];
 
@@ -188,6 +190,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
 
   // ---------- epilogue: O = acc * S / (l * 448) ----------
   if (qrow < N) {
+    if (LSE && hh == 0) LSE[(int64_t)bh * N + qrow] = row_lse(mc, l_i, sm_scale, qmu);
     const float inv = (l_i > 0.0f) ? __fdiv_rn(Sb, l_i * P_SCALE) : 0.0f;
     T* op = O + b * o_sb + hd * o_sh + (int64_t)qrow * o_sr;
 #pragma unroll
@@ -282,7 +285,7 @@ static void launch_attn_t(const AttnArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((attn_fwd_kernel<T, QK_INT8, CAUSAL>), dim3(total), dim3(AT), 0, stream,
                      (const T*)a.q, (const u8*)a.k8, a.kconst, (const u8*)a.v8t, a.s, (T*)a.o,
                      a.q_sb, a.q_sh, a.q_sr, a.o_sb, a.o_sh, a.o_sr, (int)a.H, (int)a.N,
-                     (int)a.N_pad, num_qt, span, a.sm_scale);
+                     (int)a.N_pad, num_qt, span, a.sm_scale, a.lse, a.kmean);
 }
 
 hipError_t launch_attn_fwd(const AttnArgs& a, hipStream_t stream) {

@@ -126,7 +126,7 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
                      int64_t q_sh, int64_t q_sr, const void* k8, const float* kconst,
                      const void* v8t, const float* s, void* o, int64_t o_sb, int64_t o_sh,
                      int64_t o_sr, int64_t B, int64_t H, int64_t N, int64_t N_pad, float sm_scale,
-                     int kernel, void* stream) {
+                     int kernel, float* lse, const float* kmean, void* stream) {
   if (dtype != SAGE_F16 && dtype != SAGE_BF16)
     return fail(SAGE_ERR_INVALID, "dtype: unsupported dtype code %d", dtype);
   if (dtype == SAGE_BF16 && qk_int8)
@@ -142,6 +142,10 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
     return fail(SAGE_ERR_INVALID, "sm_scale: must be positive and finite (got %g)", (double)sm_scale);
   if (kernel != SAGE_KERNEL_AUTO && kernel != SAGE_KERNEL_Q128 && kernel != SAGE_KERNEL_Q256)
     return fail(SAGE_ERR_INVALID, "kernel: unknown main-loop kernel code %d", kernel);
+  if (lse && ((uintptr_t)lse & 3u))
+    return fail(SAGE_ERR_INVALID, "ptr_align: lse must be 4-byte aligned");
+  if (kmean && !aligned16(kmean))
+    return fail(SAGE_ERR_INVALID, "ptr_align: kmean must be 16-byte aligned");
   sage::AttnArgs a;
   a.dtype = dtype;
   a.qk_int8 = qk_int8 ? 1 : 0;
@@ -163,6 +167,8 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
   a.N = N;
   a.N_pad = N_pad;
   a.sm_scale = sm_scale;
+  a.lse = lse;
+  a.kmean = lse ? kmean : nullptr;
   // The 256-query ping-pong pays off on long sequences; at short ones its larger tiles leave too
   // few blocks per CU and more causal diagonal work, and the 128-query kernel is as fast or faster.
   const bool q256 = kernel == SAGE_KERNEL_Q256 || (kernel == SAGE_KERNEL_AUTO && N >= 16384);
@@ -176,7 +182,8 @@ int sage_attn_fwd(int dtype, int qk_int8, int causal, const void* q, int64_t q_s
                   const float* s, void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr, int64_t B,
                   int64_t H, int64_t N, int64_t N_pad, float sm_scale, void* stream) {
   return sage_attn_fwd_ex(dtype, qk_int8, causal, q, q_sb, q_sh, q_sr, k8, kconst, v8t, s, o,
-                          o_sb, o_sh, o_sr, B, H, N, N_pad, sm_scale, SAGE_KERNEL_AUTO, stream);
+                          o_sb, o_sh, o_sr, B, H, N, N_pad, sm_scale, SAGE_KERNEL_AUTO, nullptr,
+                          nullptr, stream);
 }
 
 int sage_quant_q(int dtype, int qk_int8, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sr,

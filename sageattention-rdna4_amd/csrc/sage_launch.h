@@ -47,6 +47,8 @@ struct AttnArgs {
   int64_t o_sb, o_sh, o_sr;
   int64_t B, H, N, N_pad;
   float sm_scale;
+  float* lse;              // optional (B*H, N) fp32 row logsumexp
+  const float* kmean;      // optional (B*H, 128) fp32 smooth_k mean, for the logsumexp correction
 };
 hipError_t launch_attn_fwd(const AttnArgs& a, hipStream_t stream);
 // the two-group ping-pong form of the same main loop (256 queries per block of 8 waves)

@@ -36,7 +36,7 @@ ENVELOPE = dict(
     smooth_k=(False, True),
     batch_heads="B*H <= 65535",
     seq_len="N >= 1",
-    return_lse=False,
+    return_lse=(False, True),
     attn_mask=False,
     smooth_v=False,
 )
@@ -75,8 +75,6 @@ def _envelope_ok(q, k, v, tensor_layout, is_causal, sm_scale, return_lse, smooth
     `sageattention/sk1_backend/__init__.py:920-979`)."""
     if tensor_layout not in ("HND", "NHD"):
         return "layout"
-    if return_lse:
-        return "return_lse"
     if attn_mask is not None:
         return "attn_mask"
     if smooth_v:
@@ -119,7 +117,8 @@ def try_sk1_t1(q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=None, 
                smooth_k=True, smooth_v=False, attn_mask=None, strict=False, int8=None, bf16=None):
     """Run the gfx950 SK1 path if the call is inside `ENVELOPE`.
 
-    Returns `(out, None)` with `out` in the caller's layout and dtype, or `(None, reason)`.
+    Returns `(out, None)` with `out` in the caller's layout and dtype (`(out, lse)` as `out` with
+    `return_lse=True`, lse (B, H, N) fp32), or `(None, reason)`.
     `strict=True` raises instead of returning a refusal for a wrong arch or a library failure
     (envelope misses are always returned as a reason). `int8=False` selects fp8 Q.K for fp16
     inputs; `bf16` is accepted for signature compatibility (bf16 is always served).
@@ -146,7 +145,8 @@ def try_sk1_t1(q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=None, 
 
     try:
         out = sk1_forward(lib, q, k, v, tensor_layout=tensor_layout, is_causal=is_causal,
-                          sm_scale=sm_scale, smooth_k=smooth_k, int8=int8)
+                          sm_scale=sm_scale, smooth_k=smooth_k, int8=int8,
+                          return_lse=bool(return_lse))
     except Exception as e:
         if strict:
             raise
@@ -156,9 +156,12 @@ def try_sk1_t1(q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=None, 
 
 
 def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=None,
-                smooth_k=True, int8=None, events=None, kernel=0):
+                smooth_k=True, int8=None, events=None, kernel=0, return_lse=False):
     """The served path without the envelope check: allocate, prologue (2 launches), main loop.
     `kernel` picks the main-loop kernel (0: by size, 1: 128 queries per block, 2: 256).
+    With `return_lse`, returns `(out, lse)`: lse (B, H, N) fp32, each row's natural-log
+    logsumexp of its scores times sm_scale (with smooth_k, corrected by sm_scale * q . mean_k, as
+    the reference's `core.py:1437-1439`).
 
     `events`, when given, is a sequence of three `torch.cuda.Event`s recorded on the launch stream
     before the prologue, between the prologue and the main loop, and after the main loop.
@@ -182,6 +185,9 @@ def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=
     s = torch.empty(BH, device=dev, dtype=torch.float32)
     kconst = torch.empty(BH, n_pad // 64, 3, 64, device=dev, dtype=torch.float32)
     ws = torch.empty(lib.workspace_bytes(BH, N), device=dev, dtype=torch.uint8)
+    lse = torch.empty(B, H, N, device=dev, dtype=torch.float32) if return_lse else None
+    kmean = (torch.empty(BH, D, device=dev, dtype=torch.float32)
+             if (return_lse and smooth_k) else None)
     if tensor_layout == "NHD":
         out = torch.empty(B, N, H, D, device=dev, dtype=q.dtype)
         oo = out.transpose(1, 2)
@@ -191,12 +197,12 @@ def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=
     with torch.cuda.device(dev):
         if events is not None:
             events[0].record()
-        lib.kv_prologue(kk, vv, k8, sk, v8t, sv, s, None, ws, k_int8=qk_int8,
+        lib.kv_prologue(kk, vv, k8, sk, v8t, sv, s, kmean, ws, k_int8=qk_int8,
                         smooth_k=bool(smooth_k), fold=True, n_pad=n_pad, kconst=kconst)
         if events is not None:
             events[1].record()
         lib.attn_fwd(qq, k8, kconst, v8t, s, oo, qk_int8=qk_int8, causal=bool(is_causal),
-                     sm_scale=sm, n_pad=n_pad, kernel=kernel)
+                     sm_scale=sm, n_pad=n_pad, kernel=kernel, lse=lse, kmean=kmean)
         if events is not None:
             events[2].record()
-    return out
+    return (out, lse) if return_lse else out

@@ -70,7 +70,7 @@ def make(name):
         k8=bits(r["k8"]) if r["k8"].dtype != torch.int8 else r["k8"].numpy(),
         sk=r["sk"].numpy(), v8t=bits(r["v8t"]), sv=r["sv"].numpy(), s=r["s"].numpy(),
         svp=r["svp"].numpy(), q8=bits(r["q8"]) if r["q8"].dtype != torch.int8 else r["q8"].numpy(),
-        sq=r["sq"].numpy(), c_q=r["c_q"].numpy(), o=bits(r["o"]),
+        sq=r["sq"].numpy(), c_q=r["c_q"].numpy(), o=bits(r["o"]), lse=r["lse"].numpy(),
     )
     if r["mean"] is not None:
         arr["mean"] = r["mean"].numpy()

@@ -53,7 +53,7 @@ def test_oracle_reproduces_fixture(path):
     q, k, v, m = _inputs(g)
     r = oracle.emulate_sageattn(q, k, v, tensor_layout=m["layout"], is_causal=m["causal"],
                                 smooth_k=m["smooth_k"])
-    for name in ("k8", "sk", "v8t", "sv", "s", "svp", "q8", "sq", "c_q", "o"):
+    for name in ("k8", "sk", "v8t", "sv", "s", "svp", "q8", "sq", "c_q", "o", "lse"):
         assert np.array_equal(_bits(r[name]), g[name]), name
     if m["smooth_k"]:
         assert np.array_equal(r["mean"].numpy(), g["mean"])
@@ -84,8 +84,8 @@ def test_gpu_matches_fixture(path):
     lib.kv_prologue(kk, vv, k8, sk, v8t, sv, s, mean, ws, k_int8=int8, smooth_k=m["smooth_k"],
                     fold=True, n_pad=n_pad)
     q8, sq, cq = lib.quant_q(qq, float(g["sm_scale"][0]), qk_int8=int8)
-    out = sageattn(qd, kd, vd, tensor_layout=m["layout"], is_causal=m["causal"],
-                   smooth_k=m["smooth_k"])
+    out, lse = sageattn(qd, kd, vd, tensor_layout=m["layout"], is_causal=m["causal"],
+                        smooth_k=m["smooth_k"], return_lse=True)
     torch.cuda.synchronize()
     got = dict(k8=k8, v8t=v8t, sk=sk, svp=sv, s=s, q8=q8, sq=sq, c_q=cq)
     for name, t in got.items():
@@ -96,3 +96,7 @@ def test_gpu_matches_fixture(path):
     c, r1 = cosine(out.cpu(), ref), rel_l1(out.cpu(), ref)
     print("cos %.6f rel_l1 %.3e" % (c, r1), flush=True)
     assert c >= COS_MIN and r1 <= REL_L1_MAX
+    # logsumexp: same quantized scores, hardware exp2/log2 and another summation order
+    lref = torch.from_numpy(g["lse"])
+    assert lse.shape == lref.shape and lse.dtype == torch.float32
+    assert torch.allclose(lse.cpu(), lref, rtol=1e-4, atol=1e-3), (lse.cpu() - lref).abs().max()

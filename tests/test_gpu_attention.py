@@ -239,3 +239,54 @@ def test_auto_kernel_choice_serves_long_sequences():
     o_auto = _forward(q, k, v, causal=True, kernel=0)
     o128 = _forward(q, k, v, causal=True, kernel=1)
     assert torch.equal(o_auto, o128)
+
+
+# ---------------------------------------------------------------------------------------------
+# return_lse: each row's natural-log logsumexp of Q.K^T * sm_scale (the reference's `core.py`
+# `:1081-1095`, `:1437-1439`; its SK1 path refuses it). Bars: against the emulation's value from
+# the same quantized scores, rtol 1e-4 + atol 1e-3 (hardware exp2/log2, summation order); against
+# unquantized fp64 attention the quantization error is reported and held to the scheme's own on
+# these inputs (the emulation's worst row: 0.050 int8 Q.K, 0.201 fp8 Q.K; mean over rows 0.012 and
+# 0.043, all without smoothing, whose per-channel key offsets cost the quantizer its range), with
+# 1.5x margin: max 0.075 / 0.30, mean 0.018 / 0.065.
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("layout", ["HND", "NHD"])
+@pytest.mark.parametrize("smooth_k", [True, False])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N", [65, 300, 1337])
+def test_return_lse_matches_emulation(N, dtype, causal, smooth_k, layout):
+    q, k, v = make_qkv(1, 3, N, seed=N + 3, dtype=dtype, layout=layout, k_offset_std=2.0)
+    r = oracle.emulate_sageattn(q, k, v, tensor_layout=layout, is_causal=causal, smooth_k=smooth_k)
+    out, lse = _sageattn()(q.cuda(), k.cuda(), v.cuda(), tensor_layout=layout, is_causal=causal,
+                           smooth_k=smooth_k, return_lse=True)
+    torch.cuda.synchronize()
+    B, H = (1, 3)
+    assert lse.shape == (B, H, N) and lse.dtype == torch.float32
+    lse = lse.cpu()
+    assert torch.isfinite(lse).all()
+    err = (lse - r["lse"]).abs()
+    assert torch.allclose(lse, r["lse"], rtol=1e-4, atol=1e-3), err.max().item()
+    assert cosine(out.cpu(), r["o"]) >= COS_MIN and rel_l1(out.cpu(), r["o"]) <= REL_L1_MAX
+    ex = oracle.exact_lse(q, k, is_causal=causal, tensor_layout=layout).float()
+    qerr = (lse - ex).abs()
+    print("lse: vs emulation %.2e, vs exact %.3e (mean %.3e)"
+          % (err.max().item(), qerr.max().item(), qerr.mean().item()))
+    int8_qk = dtype == torch.float16
+    assert qerr.max().item() < (0.075 if int8_qk else 0.30), qerr.max().item()
+    assert qerr.mean().item() < (0.018 if int8_qk else 0.065), qerr.mean().item()
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_return_lse_same_output_and_both_kernels(causal):
+    from sageattention.sk1_backend import sk1_forward
+    from sageattention.sk1_backend.sk1_loader import SageLib
+    q, k, v = make_qkv(1, 2, 1000, seed=31, dtype=torch.float16, k_offset_std=2.0)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    lib = SageLib.get()
+    o_plain = sk1_forward(lib, qd, kd, vd, is_causal=causal, kernel=1)
+    o1, l1 = sk1_forward(lib, qd, kd, vd, is_causal=causal, kernel=1, return_lse=True)
+    o2, l2 = sk1_forward(lib, qd, kd, vd, is_causal=causal, kernel=2, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o_plain, o1)            # asking for the logsumexp changes nothing else
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)

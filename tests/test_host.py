@@ -66,8 +66,12 @@ def test_library_host_calls_without_a_gpu():
     p16 = ctypes.c_void_p(16)
     rc = L.lib.sage_attn_fwd_ex(0, 1, 0, p16, 12800, 12800, 128, p16, p16, p16, p16,
                                 p16, 12800, 12800, 128, 1, 1, 100, 128, ctypes.c_float(0.1), 7,
-                                None)
+                                None, None, None)
     assert rc == 1 and b"kernel" in L.lib.sage_last_error()
+    rc = L.lib.sage_attn_fwd_ex(0, 1, 0, p16, 12800, 12800, 128, p16, p16, p16, p16,
+                                p16, 12800, 12800, 128, 1, 1, 100, 128, ctypes.c_float(0.1), 0,
+                                ctypes.c_void_p(18), None, None)
+    assert rc == 1 and b"lse must be 4-byte aligned" in L.lib.sage_last_error()
 
 
 def test_strided_view_reason_rule():
@@ -96,7 +100,9 @@ def test_envelope_reasons_on_cpu_tensors():
     args = dict(tensor_layout="HND", is_causal=False, sm_scale=None, return_lse=False,
                 smooth_k=True, smooth_v=False, attn_mask=None)
     assert _envelope_ok(q, q, q, **dict(args, tensor_layout="BHND")) == "layout"
-    assert _envelope_ok(q, q, q, **dict(args, return_lse=True)) == "return_lse"
+    # return_lse is served here (the reference's SK1 path refuses it): CPU tensors then fail
+    # on the device check, not on return_lse
+    assert _envelope_ok(q, q, q, **dict(args, return_lse=True)) == "device"
     assert _envelope_ok(q, q, q, **dict(args, smooth_v=True)) == "smooth_v"
     assert _envelope_ok(q, q, q, **dict(args, attn_mask=torch.ones(1))) == "attn_mask"
     assert _envelope_ok(q, q, q, **args) == "device"
@@ -120,7 +126,7 @@ def test_try_sk1_t1_returns_reasons():
     from sageattention.sk1_backend import try_sk1_t1
     q = torch.empty(1, 2, 10, 128, dtype=torch.float16)
     assert try_sk1_t1(q, q, q) == (None, "device")
-    assert try_sk1_t1(q, q, q, return_lse=True) == (None, "return_lse")
+    assert try_sk1_t1(q, q, q, return_lse=True) == (None, "device")
 
 
 def test_arch_gate_is_monkeypatchable(monkeypatch):

@@ -272,6 +272,79 @@ def test_uniform_keys_give_the_mean_of_v():
     assert (r["o"][0, 0].float() - mean_v).abs().max().item() < 0.02
 
 
+# ----------------------------------------------------------------------------- logsumexp
+def _scores_fp32(q8r, cqr, k8, sk, row, N, causal):
+    """The emulated scores of one row (A.9) as fp32 scalars, masked keys dropped."""
+    f32 = np.float32
+    out = []
+    for n in range(k8.shape[0]):
+        dead = (n > row) if causal else (n >= N)
+        if dead:
+            continue
+        dot = f32(float(np.dot(q8r.astype(np.float64), k8[n].astype(np.float64))))
+        out.append(float(f32(dot * f32(cqr * sk[n]))))
+    return out
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("N", [5, 64, 130])
+def test_lse_vs_brute_force(N, causal):
+    # log2 sum exp2 of the row's scores straight from their definition (fp64, no tiles, no
+    # running max) against the tiled bookkeeping m_use + log2(l).
+    q, k, v = make_qkv(1, 1, N, seed=N + 1, k_offset_std=1.0)
+    r = oracle.emulate_sageattn(q, k, v, is_causal=causal, smooth_k=False)
+    k8 = r["k8"][0].numpy().astype(np.int32)
+    q8 = r["q8"][0].numpy().astype(np.int32)
+    for row in sorted({0, 1, N // 2, N - 1}):
+        sc = _scores_fp32(q8[row], r["c_q"][0, row].item(), k8, r["sk"][0].numpy(), row, N, causal)
+        mx = max(sc)
+        lse2 = mx + math.log2(sum(2.0 ** (x - mx) for x in sc))
+        got = r["lse"][0, 0, row].item()
+        assert abs(got - lse2 / 1.44269504) < 2e-5 * max(1.0, abs(got)), (row, got, lse2)
+
+
+def test_lse_causal_first_row_closed_form():
+    # Row 0 of a causal call sees only key 0: m = s[0,0], l = 1, so lse = s[0,0] / 1.44269504
+    # (+ the smooth_k correction sm_scale * q[0] . mean).
+    q, k, v = make_qkv(1, 2, 70, seed=9, k_offset_std=2.0)
+    r = oracle.emulate_sageattn(q, k, v, is_causal=True, smooth_k=True)
+    for bh in range(2):
+        s00 = _scores_fp32(r["q8"][bh, 0].numpy().astype(np.int32), r["c_q"][bh, 0].item(),
+                           r["k8"][bh].numpy().astype(np.int32), r["sk"][bh].numpy(), 0, 70, True)
+        assert len(s00) == 1
+        corr = float(torch.dot(q[0, bh, 0].float(), r["mean"][bh]).item()) * r["sm_scale"]
+        want = s00[0] / 1.44269504 + corr
+        assert abs(r["lse"][0, bh, 0].item() - want) < 1e-4, (bh, r["lse"][0, bh, 0].item(), want)
+
+
+def test_lse_uniform_keys_closed_form():
+    # Identical keys: every score of a row equals c, so lse = (c + log2(N)) / 1.44269504.
+    N = 200
+    q, k, v = make_qkv(1, 1, N, seed=6)
+    k[:] = k[:, :, :1]
+    r = oracle.emulate_sageattn(q, k, v, is_causal=False, smooth_k=False)
+    for row in (0, 17, N - 1):
+        c = _scores_fp32(r["q8"][0, row].numpy().astype(np.int32), r["c_q"][0, row].item(),
+                         r["k8"][0].numpy().astype(np.int32), r["sk"][0].numpy(), row, N, False)
+        assert len(set(c)) == 1
+        want = (c[0] + math.log2(N)) / 1.44269504
+        assert abs(r["lse"][0, 0, row].item() - want) < 1e-4
+
+
+def test_lse_close_to_exact_and_needs_the_correction():
+    # With a K channel offset (mean ~ N(0, 2)), smoothing shifts every score of a row by
+    # sm_scale * q . mean; the corrected logsumexp must track the unquantized one, and the same
+    # value without the correction must not.
+    q, k, v = make_qkv(1, 2, 300, seed=12, k_offset_std=2.0)
+    for causal in (False, True):
+        r = oracle.emulate_sageattn(q, k, v, is_causal=causal, smooth_k=True)
+        ex = oracle.exact_lse(q, k, is_causal=causal).float()
+        err = (r["lse"] - ex).abs()
+        assert err.max().item() < 0.05, err.max().item()
+        corr = torch.matmul(q[0].float(), r["mean"][:, :, None]).squeeze(-1) * r["sm_scale"]
+        assert (r["lse"][0] - corr - ex[0]).abs().max().item() > 0.5
+
+
 def test_emulation_close_to_exact_attention():
     # The scheme's error against exact attention on N(0,1) inputs: the reference's bar is 0.08
     # relative RMS (`tests/test_sk1_backend.py:28-29`), observed 0.03-0.055.
