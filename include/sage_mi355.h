@@ -102,24 +102,35 @@ int sage_attn_fwd(int dtype, int qk_int8, int causal,
                   int64_t B, int64_t H, int64_t N, int64_t N_pad, float sm_scale, void* stream);
 
 /*
- * sage_attn_fwd with the main-loop kernel chosen by the caller (SAGE_KERNEL_*) and an optional
- * per-row logsumexp; sage_attn_fwd is this with SAGE_KERNEL_AUTO and no logsumexp. Both kernels
- * compute the same arithmetic in the same order per query; only the block shape and schedule
- * differ. The kernel choice has no counterpart in the reference (one kernel per dtype there).
+ * sage_attn_fwd generalized: grouped K/V heads, a key length of its own, the main-loop kernel
+ * chosen by the caller (SAGE_KERNEL_*) and an optional per-row logsumexp. sage_attn_fwd is this
+ * with H_kv = H, N_kv = N, SAGE_KERNEL_AUTO and no logsumexp. Both kernels compute the same
+ * arithmetic in the same order per query; only the block shape and schedule differ. The kernel
+ * choice has no counterpart in the reference (one kernel per dtype there).
+ *
+ *   q, o      logical (B, H, N, 128) views, as in sage_attn_fwd
+ *   k8, kconst, v8t, s   the prologue's outputs for B*H_kv planes of N_kv keys (N_kv_pad =
+ *             ceil(N_kv/64)*64). Query head h reads K/V head h / (H / H_kv) (grouped-query and
+ *             multi-query attention; H must be a multiple of H_kv), and N may differ from N_kv
+ *             when not causal. The reference's SK1 envelope refuses both
+ *             (`sageattention/sk1_backend/__init__.py:966-978`); its upstream API serves them
+ *             (`sageattention/core.py:824-829`: H % H_kv == 0, causal only with N == N_kv),
+ *             and so does this entry point.
  *
  *   lse    optional (B*H, N) fp32: the natural-log logsumexp of each row's scores times sm_scale,
  *          as `sageattn(..., return_lse=True)` returns it (`core.py:1081-1095`, `:1437-1439` of
  *          the reference): (RN(c_q*m) + log2 l) / 1.44269504 over the quantized scores, plus
  *          sm_scale * (q . kmean) when kmean is given. The reference's SK1 kernels refuse
  *          return_lse (`sageattention/sk1_backend/__init__.py:925-926`); this fills that row.
- *   kmean  optional (B*H, 128) fp32: the smooth_k mean the prologue subtracted (its `mean`
+ *   kmean  optional (B*H_kv, 128) fp32: the smooth_k mean the prologue subtracted (its `mean`
  *          output); used only with lse.
  */
 int sage_attn_fwd_ex(int dtype, int qk_int8, int causal,
                      const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sr,
                      const void* k8, const float* kconst, const void* v8t, const float* s,
                      void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr,
-                     int64_t B, int64_t H, int64_t N, int64_t N_pad, float sm_scale, int kernel,
+                     int64_t B, int64_t H, int64_t N, int64_t H_kv, int64_t N_kv,
+                     int64_t N_kv_pad, float sm_scale, int kernel,
                      float* lse, const float* kmean, void* stream);
 
 /*

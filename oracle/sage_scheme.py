@@ -234,9 +234,24 @@ def row_lse(lse2, q, mean, sm_scale):
     """
     lse = lse2 / torch.tensor(1.44269504, dtype=torch.float32)
     if mean is not None:
-        corr = torch.matmul(q.to(torch.float32), mean[:, :, None]).squeeze(-1)
+        # q . mean in fp64 (each fp16/bf16 x fp32 product is exact there), rounded once to fp32:
+        # independent of how many rows one call holds, unlike an fp32 matmul's blocking
+        corr = torch.matmul(q.to(torch.float64), mean.to(torch.float64)[:, :, None]).squeeze(-1)
+        corr = corr.to(torch.float32)
         lse = lse + corr * torch.tensor(sm_scale, dtype=torch.float32)
     return lse
+
+
+def kv_planes(B, H, H_kv, N, N_kv, is_causal):
+    """For each query plane b*H + h, the K/V plane it reads: b*H_kv + h // (H // H_kv) (grouped-
+    query attention, the upstream API's rule, `sageattention/core.py:824-829` of the reference,
+    which also raises for H not a multiple of H_kv and for causal calls with N != N_kv)."""
+    if H_kv < 1 or H % H_kv != 0:
+        raise ValueError("num_qo_heads must be divisible by num_kv_heads.")
+    if is_causal and N != N_kv:
+        raise ValueError("causal attention requires q_len == kv_len.")
+    g = H // H_kv
+    return (torch.arange(B)[:, None] * H_kv + torch.arange(H)[None, :] // g).reshape(-1)
 
 
 def emulate_sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=None, smooth_k=True,
@@ -247,31 +262,48 @@ def emulate_sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=Non
     (`sk1_t6i`), bf16 inputs use fp8 Q.K (`sk1_t4a1sb`); `qk_int8=False` forces the fp8 form for
     fp16 inputs. `sm_scale` defaults to `D ** -0.5` (`__init__.py:1165`).
 
+    k and v may have H_kv heads (H a multiple of H_kv) and N_kv rows (N_kv == N when causal):
+    query plane b*H + h reads K/V plane `kv_planes(...)[b*H + h]`.
+
     Returns a dict with `mean, k8, sk, v8t, sv, s, svp, q8, sq, c_q, o, lse` where `o` has the
-    caller's layout and dtype, `lse` is (B, H, N) fp32 (the `return_lse` output) and every other
-    tensor is per (b, h) plane, (BH, ...).
+    caller's layout and dtype, `lse` is (B, H, N) fp32 (the `return_lse` output), `q8, sq, c_q`
+    are per query plane (B*H, ...) and `mean, k8, sk, v8t, sv, s, svp` per K/V plane
+    (B*H_kv, ...).
     """
     qq, kk, vv = (to_hnd(t, tensor_layout) for t in (q, k, v))
     B, H, N, D = qq.shape
+    H_kv, N_kv = kk.shape[1], kk.shape[2]
+    kvp = kv_planes(B, H, H_kv, N, N_kv, is_causal)
     BH = B * H
     if qk_int8 is None:
         qk_int8 = (q.dtype == torch.float16)
     sm = float(sm_scale if sm_scale is not None else D ** -0.5)
-    n_pad = n_pad_for(N)
-    qr, kr, vr = (t.reshape(BH, N, D) for t in (qq, kk, vv))
+    n_pad = n_pad_for(N_kv)
+    qr = qq.reshape(BH, N, D)
+    kr, vr = (t.reshape(B * H_kv, N_kv, D) for t in (kk, vv))
     mean = kseq_mean(kr) if smooth_k else None
     k8, sk = quant_k(kr, n_pad, mean=mean, int8=qk_int8)
     v8t, sv = quant_v(vr, n_pad)
     s, svp = fold_v_scale(sv)
     q8, sq, c_q = quant_q(qr, sm, int8=qk_int8)
     lse2 = torch.empty(BH, N, dtype=torch.float32)
-    o = attention_tiles(q8, c_q, k8, sk, v8t, svp, s, N, is_causal, q.dtype, lse_out=lse2)
+    o = attention_tiles(q8, c_q, k8[kvp], sk[kvp], v8t[kvp], svp[kvp], s[kvp], N_kv, is_causal,
+                        q.dtype, lse_out=lse2)
     o = o.view(B, H, N, D)
     if tensor_layout == "NHD":
         o = o.transpose(1, 2).contiguous()
-    lse = row_lse(lse2, qr, mean, sm).view(B, H, N)
+    lse = row_lse(lse2, qr, None if mean is None else mean[kvp], sm).view(B, H, N)
     return dict(mean=mean, k8=k8, sk=sk, v8t=v8t, sv=sv, s=s, svp=svp, q8=q8, sq=sq, c_q=c_q, o=o,
                 lse=lse, n_pad=n_pad, sm_scale=sm)
+
+
+def _expand_kv_heads(x, H):
+    """(B, H_kv, N_kv, D) -> (B, H, N_kv, D): query head h sees K/V head h // (H // H_kv)."""
+    if x.shape[1] == H:
+        return x
+    if H % x.shape[1]:
+        raise ValueError("num_qo_heads must be divisible by num_kv_heads.")
+    return x.repeat_interleave(H // x.shape[1], dim=1)
 
 
 def exact_lse(q, k, is_causal=False, sm_scale=None, tensor_layout="HND", q_chunk=1024):
@@ -280,13 +312,14 @@ def exact_lse(q, k, is_causal=False, sm_scale=None, tensor_layout="HND", q_chunk
     Returns (B, H, N) fp64."""
     qq, kk = (to_hnd(t, tensor_layout).to(torch.float64) for t in (q, k))
     B, H, N, D = qq.shape
+    kk = _expand_kv_heads(kk, H)
     sm = float(sm_scale if sm_scale is not None else D ** -0.5)
     out = torch.empty(B, H, N, dtype=torch.float64)
     for r0 in range(0, N, q_chunk):
         r1 = min(N, r0 + q_chunk)
         s = torch.matmul(qq[:, :, r0:r1], kk.transpose(2, 3)) * sm
         if is_causal:
-            dead = torch.arange(N)[None, :] > torch.arange(r0, r1)[:, None]
+            dead = torch.arange(kk.shape[2])[None, :] > torch.arange(r0, r1)[:, None]
             s = s.masked_fill(dead, -math.inf)
         out[:, :, r0:r1] = torch.logsumexp(s, dim=-1)
     return out
@@ -299,13 +332,14 @@ def exact_attention(q, k, v, is_causal=False, sm_scale=None, tensor_layout="HND"
     """
     qq, kk, vv = (to_hnd(t, tensor_layout).to(torch.float64) for t in (q, k, v))
     B, H, N, D = qq.shape
+    kk, vv = _expand_kv_heads(kk, H), _expand_kv_heads(vv, H)
     sm = float(sm_scale if sm_scale is not None else D ** -0.5)
     out = torch.empty(B, H, N, D, dtype=torch.float64)
     for r0 in range(0, N, q_chunk):
         r1 = min(N, r0 + q_chunk)
         s = torch.matmul(qq[:, :, r0:r1], kk.transpose(2, 3)) * sm
         if is_causal:
-            dead = torch.arange(N)[None, :] > torch.arange(r0, r1)[:, None]
+            dead = torch.arange(kk.shape[2])[None, :] > torch.arange(r0, r1)[:, None]
             s = s.masked_fill(dead, -math.inf)
         out[:, :, r0:r1] = torch.matmul(torch.softmax(s, dim=-1), vv)
     if tensor_layout == "NHD":

@@ -285,8 +285,14 @@ __device__ __forceinline__ BlockShift scores_block(f32x16 (&sx)[2], float sk0, f
   const float mx = max_halves(max32(x));
   const float m_new = fmaxf(m_x, mx);
   float mc_new = cq * ((m_new == -INFINITY) ? 0.0f : m_new);
+  // One to two ulps below RN(c_q * m): the max key's exp2 argument c_q*m - mc (exact in the fma)
+  // is then never negative, and probs_block clamps its exp2 to at most 1, so the max key gets
+  // p = 1 exactly, as the reference's exp2(s - m) does. (With the shift RN(c_q*m) the argument
+  // is the product's rounding residual, +-1e-6, and p*W can then round to the other side of an
+  // e4m3 tie: a 6-8% change of the dominant key's weight.) 0 stays 0.
+  mc_new = __builtin_fmaf(__builtin_fabsf(mc_new), -0x1p-23f, mc_new);
   // mc_new is rounded before it is used: the opaque copy keeps the compiler from fusing the
-  // product into the subtraction below, which it would do or not depending on the surrounding
+  // products into the subtraction below, which it would do or not depending on the surrounding
   // code (so two kernels would round alpha differently). exp2(mc - mc_new) of the rounded shifts
   // is then exactly 1 for an unmoved max; the select skips the exp2 there.
   asm volatile("" : "+v"(mc_new));
@@ -322,7 +328,9 @@ __device__ __forceinline__ void probs_block(const f32x16 (&x)[2], float w0, floa
     static_for<0, 4>([&](auto ec) {
       constexpr int e = decltype(ec)::value;
       constexpr int jj = 4 * k4 + e;
-      p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[jj >> 4][jj & 15], cq, -sh.mc));
+      // min(exp2, 1) through the VOP3 clamp bit of v_exp_f32 (no extra instruction)
+      p[e] = __builtin_amdgcn_fmed3f(
+          __builtin_amdgcn_exp2f(__builtin_fmaf(x[jj >> 4][jj & 15], cq, -sh.mc)), 0.0f, 1.0f);
       ps[e] = k4 ? ps[e] + p[e] : p[e];
       p[e] *= row_bcast<jj & 15>(jj < 16 ? w0 : w1);
     });

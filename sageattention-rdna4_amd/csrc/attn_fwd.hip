@@ -41,8 +41,8 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
     const T* __restrict__ Q, const u8* __restrict__ K8, const float* __restrict__ KC,
     const u8* __restrict__ V8T, const float* __restrict__ Sfold,
     T* __restrict__ O, int64_t q_sb, int64_t q_sh, int64_t q_sr, int64_t o_sb, int64_t o_sh,
-    int64_t o_sr, int H, int N, int N_pad, int num_qt, int xcd_span, float sm_scale,
-    float* __restrict__ LSE, const float* __restrict__ KMEAN) {
+    int64_t o_sr, int H, int H_kv, int G, int N, int Nk, int Nk_pad, int num_qt, int xcd_span,
+    float sm_scale, float* __restrict__ LSE, const float* __restrict__ KMEAN) {
   // Three staging buffers (K tile, V^T tile, per-key constants), declared as separate objects:
   // with the buffer chosen at compile time the compiler can tell a DMA into one buffer from reads
   // of another, and waits for a DMA only where its own buffer is read. (Its wait bookkeeping
@@ -58,6 +58,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
   int qt = id - bh * num_qt;
   if (CAUSAL) qt = num_qt - 1 - qt;
   const int b = bh / H, hd = bh - b * H;
+  const int kvp = b * H_kv + hd / G;   // the K/V plane this query plane reads (GQA: G heads share it)
 
   // w is wave-uniform; readfirstlane tells the compiler so, which turns every per-wave decision
   // (causal block skipping) into a scalar branch rather than an EXEC mask.
@@ -66,11 +67,11 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
   const int q0 = qt * BM + w * 32;
   const int qrow = q0 + l32;
 
-  const u8* Kb = K8 + (int64_t)bh * N_pad * HD;
-  const u8* Vb = V8T + (int64_t)bh * HD * N_pad;
-  const float* KCb = KC + (int64_t)bh * N_pad * 3;   // 192 floats per 64-key block
+  const u8* Kb = K8 + (int64_t)kvp * Nk_pad * HD;
+  const u8* Vb = V8T + (int64_t)kvp * HD * Nk_pad;
+  const float* KCb = KC + (int64_t)kvp * Nk_pad * 3;   // 192 floats per 64-key block
 
-  const int n_blocks = N_pad / BK;
+  const int n_blocks = Nk_pad / BK;
   const int j_end = CAUSAL ? min(n_blocks, (qt * BM + BM - 1) / BK + 1) : n_blocks;
   const int w_end = CAUSAL ? min(j_end, (q0 + 31) / BK + 1) : j_end;
 
@@ -92,7 +93,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
     const int krow = 8 * I + (lane >> 3), kpos = lane & 7;
     k_off[i] = (uint32_t)(krow * HD + 16 * (kpos ^ kswz(krow)));
     const int d = 16 * I + (lane >> 2), vpos = lane & 3;
-    v_off[i] = (uint32_t)(d * N_pad + 16 * (vpos ^ vswz(d)));
+    v_off[i] = (uint32_t)(d * Nk_pad + 16 * (vpos ^ vswz(d)));
   }
   const uint32_t c_off = (uint32_t)(4 * (64 * (w == 3 ? 0 : w) + lane));
   const uint32_t c_dst = (uint32_t)(256 * w);
@@ -117,9 +118,9 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
   float sq, cq;
   float qmu = 0.0f;   // q . mu for the logsumexp's smooth_k correction (when asked)
   quant_q_row<T, QK_INT8>(Q + b * q_sb + hd * q_sh + (int64_t)qrow * q_sr, qrow < N, hh, sm_scale,
-                          qf, sq, cq, (LSE && KMEAN) ? KMEAN + (int64_t)bh * HD : nullptr, &qmu);
+                          qf, sq, cq, (LSE && KMEAN) ? KMEAN + (int64_t)kvp * HD : nullptr, &qmu);
   (void)sq;
-  const float Sb = Sfold[bh];
+  const float Sb = Sfold[kvp];
 
   f32x16 acc[4];
 #pragma unroll
@@ -160,7 +161,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
       f32x16 st[2];
       qk_block<QK_INT8>(kcur, qf, krow0, krow1, ksw0, ksw1, hh, st);
       i32x8 pb;
-      softmax_block<QK_INT8, CAUSAL>(st, kc, j, q0, qrow, N, hh, cq, m_x, mc, l_i, acc, pb);
+      softmax_block<QK_INT8, CAUSAL>(st, kc, j, q0, qrow, Nk, hh, cq, m_x, mc, l_i, acc, pb);
 
       // ---------- O^T += V^T . P^T ----------
 #pragma unroll
@@ -284,8 +285,9 @@ static void launch_attn_t(const AttnArgs& a, hipStream_t stream) {
   const int span = (total / 8) * 8;
   hipLaunchKernelGGL((attn_fwd_kernel<T, QK_INT8, CAUSAL>), dim3(total), dim3(AT), 0, stream,
                      (const T*)a.q, (const u8*)a.k8, a.kconst, (const u8*)a.v8t, a.s, (T*)a.o,
-                     a.q_sb, a.q_sh, a.q_sr, a.o_sb, a.o_sh, a.o_sr, (int)a.H, (int)a.N,
-                     (int)a.N_pad, num_qt, span, a.sm_scale, a.lse, a.kmean);
+                     a.q_sb, a.q_sh, a.q_sr, a.o_sb, a.o_sh, a.o_sr, (int)a.H, (int)a.H_kv,
+                     (int)(a.H / a.H_kv), (int)a.N, (int)a.N_kv, (int)a.N_kv_pad, num_qt, span,
+                     a.sm_scale, a.lse, a.kmean);
 }
 
 hipError_t launch_attn_fwd(const AttnArgs& a, hipStream_t stream) {

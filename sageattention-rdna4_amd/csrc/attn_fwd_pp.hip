@@ -34,8 +34,8 @@ template <typename T, bool QK_INT8, bool CAUSAL>
 __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_pp_kernel(
     const T* __restrict__ Q, const u8* __restrict__ K8, const float* __restrict__ KC,
     const u8* __restrict__ V8T, const float* __restrict__ Sfold, T* __restrict__ O, int64_t q_sb,
-    int64_t q_sh, int64_t q_sr, int64_t o_sb, int64_t o_sh, int64_t o_sr, int H, int N, int N_pad,
-    int num_qt, int xcd_span, float sm_scale,
+    int64_t q_sh, int64_t q_sr, int64_t o_sb, int64_t o_sh, int64_t o_sr, int H, int H_kv, int G,
+    int N, int Nk, int Nk_pad, int num_qt, int xcd_span, float sm_scale,
     float* __restrict__ LSE, const float* __restrict__ KMEAN) {
   __shared__ StageBuf sB[3];
   using I0 = std::integral_constant<int, 0>;
@@ -49,6 +49,7 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
   int qt = id - bh * num_qt;
   if (CAUSAL) qt = num_qt - 1 - qt;
   const int b = bh / H, hd = bh - b * H;
+  const int kvp = b * H_kv + hd / G;   // the K/V plane this query plane reads (GQA: G heads share it)
 
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = w >> 2, s = w & 3;
@@ -56,11 +57,11 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
   const int q0 = qt * PP_BM + 64 * s + 32 * g;
   const int qrow = q0 + l32;
 
-  const u8* Kb = K8 + (int64_t)bh * N_pad * HD;
-  const u8* Vb = V8T + (int64_t)bh * HD * N_pad;
-  const float* KCb = KC + (int64_t)bh * N_pad * 3;   // 192 floats per 64-key block
+  const u8* Kb = K8 + (int64_t)kvp * Nk_pad * HD;
+  const u8* Vb = V8T + (int64_t)kvp * HD * Nk_pad;
+  const float* KCb = KC + (int64_t)kvp * Nk_pad * 3;   // 192 floats per 64-key block
 
-  const int n_blocks = N_pad / BK;
+  const int n_blocks = Nk_pad / BK;
   const int j_end = CAUSAL ? min(n_blocks, (qt * PP_BM + PP_BM - 1) / BK + 1) : n_blocks;
   // blocks this wave computes: 0 .. w_end-1 (the rest of its 2 * j_end barriers it only stages)
   const int w_end = CAUSAL ? min(j_end, (q0 + 31) / BK + 1) : j_end;
@@ -71,7 +72,7 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
   const int krow = 8 * w + (lane >> 3), kpos = lane & 7;
   const uint32_t k_off = (uint32_t)(krow * HD + 16 * (kpos ^ kswz(krow)));
   const int vd = 16 * w + (lane >> 2), vpos = lane & 3;
-  const uint32_t v_off = (uint32_t)(vd * N_pad + 16 * (vpos ^ vswz(vd)));
+  const uint32_t v_off = (uint32_t)(vd * Nk_pad + 16 * (vpos ^ vswz(vd)));
   const uint32_t c_off = (uint32_t)(4 * (64 * w + lane));
   const uint32_t lds0 = lds_addr(&sB[0]) + 1024 * w;
   // block j's tiles into buffer p: K (one request per wave), then V^T and constants (one or two).
@@ -97,9 +98,9 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
   float sq, cq;
   float qmu = 0.0f;   // q . mu for the logsumexp's smooth_k correction (when asked)
   quant_q_row<T, QK_INT8>(Q + b * q_sb + hd * q_sh + (int64_t)qrow * q_sr, qrow < N, hh, sm_scale,
-                          qf, sq, cq, (LSE && KMEAN) ? KMEAN + (int64_t)bh * HD : nullptr, &qmu);
+                          qf, sq, cq, (LSE && KMEAN) ? KMEAN + (int64_t)kvp * HD : nullptr, &qmu);
   (void)sq;
-  const float Sb = Sfold[bh];
+  const float Sb = Sfold[kvp];
 
   f32x16 acc[4];
 #pragma unroll
@@ -157,7 +158,7 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
   auto softmax = [&](const int j) {
     __builtin_amdgcn_s_setprio(1);
     const BlockShift sh =
-        scores_block<QK_INT8, CAUSAL>(st, kcp.sk0, kcp.sk1, j, q0, qrow, N, hh, cq, m_x, mc);
+        scores_block<QK_INT8, CAUSAL>(st, kcp.sk0, kcp.sk1, j, q0, qrow, Nk, hh, cq, m_x, mc);
     probs_block<false>(st, kcp.w0, kcp.w1, cq, sh, l_i, acc, pb);
     alpha_pend = sh.alpha;
     __builtin_amdgcn_s_setprio(0);
@@ -295,8 +296,9 @@ static void launch_pp_t(const AttnArgs& a, hipStream_t stream) {
   const int span = (total / 8) * 8;
   hipLaunchKernelGGL((attn_fwd_pp_kernel<T, QK_INT8, CAUSAL>), dim3(total), dim3(PP_T), 0, stream,
                      (const T*)a.q, (const u8*)a.k8, a.kconst, (const u8*)a.v8t, a.s, (T*)a.o,
-                     a.q_sb, a.q_sh, a.q_sr, a.o_sb, a.o_sh, a.o_sr, (int)a.H, (int)a.N,
-                     (int)a.N_pad, num_qt, span, a.sm_scale, a.lse, a.kmean);
+                     a.q_sb, a.q_sh, a.q_sr, a.o_sb, a.o_sh, a.o_sr, (int)a.H, (int)a.H_kv,
+                     (int)(a.H / a.H_kv), (int)a.N, (int)a.N_kv, (int)a.N_kv_pad, num_qt, span,
+                     a.sm_scale, a.lse, a.kmean);
 }
 
 hipError_t launch_attn_fwd_pp(const AttnArgs& a, hipStream_t stream) {

@@ -125,14 +125,22 @@ int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int fold, const void* 
 int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t q_sb,
                      int64_t q_sh, int64_t q_sr, const void* k8, const float* kconst,
                      const void* v8t, const float* s, void* o, int64_t o_sb, int64_t o_sh,
-                     int64_t o_sr, int64_t B, int64_t H, int64_t N, int64_t N_pad, float sm_scale,
-                     int kernel, float* lse, const float* kmean, void* stream) {
+                     int64_t o_sr, int64_t B, int64_t H, int64_t N, int64_t H_kv, int64_t N_kv,
+                     int64_t N_kv_pad, float sm_scale, int kernel, float* lse,
+                     const float* kmean, void* stream) {
   if (dtype != SAGE_F16 && dtype != SAGE_BF16)
     return fail(SAGE_ERR_INVALID, "dtype: unsupported dtype code %d", dtype);
   if (dtype == SAGE_BF16 && qk_int8)
     return fail(SAGE_ERR_INVALID, "bf16_int8: int8 Q.K is served for fp16 inputs only");
-  int rc = check_shape(B, H, N, N_pad);
+  int rc = check_shape(B, H, N, (N + 63) / 64 * 64);
   if (rc) return rc;
+  if (H_kv < 1 || H % H_kv != 0)
+    return fail(SAGE_ERR_INVALID, "heads: H (%lld) must be a multiple of H_kv (%lld)",
+                (long long)H, (long long)H_kv);
+  if ((rc = check_shape(B, H_kv, N_kv, N_kv_pad))) return rc;
+  if (causal && N != N_kv)
+    return fail(SAGE_ERR_INVALID, "seq_len: causal attention needs N == N_kv (N=%lld N_kv=%lld)",
+                (long long)N, (long long)N_kv);
   if ((rc = check_view("q", q, q_sb, q_sh, q_sr))) return rc;
   if ((rc = check_view("o", o, o_sb, o_sh, o_sr))) return rc;
   if (!k8 || !kconst || !v8t || !s) return fail(SAGE_ERR_INVALID, "an input pointer is NULL");
@@ -165,13 +173,16 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
   a.B = B;
   a.H = H;
   a.N = N;
-  a.N_pad = N_pad;
+  a.H_kv = H_kv;
+  a.N_kv = N_kv;
+  a.N_kv_pad = N_kv_pad;
   a.sm_scale = sm_scale;
   a.lse = lse;
   a.kmean = lse ? kmean : nullptr;
   // The 256-query ping-pong pays off on long sequences; at short ones its larger tiles leave too
   // few blocks per CU and more causal diagonal work, and the 128-query kernel is as fast or faster.
-  const bool q256 = kernel == SAGE_KERNEL_Q256 || (kernel == SAGE_KERNEL_AUTO && N >= 16384);
+  const bool q256 = kernel == SAGE_KERNEL_Q256 ||
+                    (kernel == SAGE_KERNEL_AUTO && N >= 16384 && N_kv >= 16384);
   return hip_status(q256 ? sage::launch_attn_fwd_pp(a, (hipStream_t)stream)
                          : sage::launch_attn_fwd(a, (hipStream_t)stream),
                     "sage_attn_fwd launch");
@@ -182,8 +193,8 @@ int sage_attn_fwd(int dtype, int qk_int8, int causal, const void* q, int64_t q_s
                   const float* s, void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr, int64_t B,
                   int64_t H, int64_t N, int64_t N_pad, float sm_scale, void* stream) {
   return sage_attn_fwd_ex(dtype, qk_int8, causal, q, q_sb, q_sh, q_sr, k8, kconst, v8t, s, o,
-                          o_sb, o_sh, o_sr, B, H, N, N_pad, sm_scale, SAGE_KERNEL_AUTO, nullptr,
-                          nullptr, stream);
+                          o_sb, o_sh, o_sr, B, H, N, H, N, N_pad, sm_scale, SAGE_KERNEL_AUTO,
+                          nullptr, nullptr, stream);
 }
 
 int sage_quant_q(int dtype, int qk_int8, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sr,

@@ -45,10 +45,11 @@ struct AttnArgs {
   const float* s;
   void* o;
   int64_t o_sb, o_sh, o_sr;
-  int64_t B, H, N, N_pad;
+  int64_t B, H, N;          // query side: B*H planes of N rows
+  int64_t H_kv, N_kv, N_kv_pad;   // key/value side: B*H_kv planes of N_kv rows (H % H_kv == 0)
   float sm_scale;
   float* lse;              // optional (B*H, N) fp32 row logsumexp
-  const float* kmean;      // optional (B*H, 128) fp32 smooth_k mean, for the logsumexp correction
+  const float* kmean;      // optional (B*H_kv, 128) fp32 smooth_k mean, for the logsumexp correction
 };
 hipError_t launch_attn_fwd(const AttnArgs& a, hipStream_t stream);
 // the two-group ping-pong form of the same main loop (256 queries per block of 8 waves)

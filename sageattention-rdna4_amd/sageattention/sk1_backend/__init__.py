@@ -35,7 +35,8 @@ ENVELOPE = dict(
     causal=(0, 1),
     smooth_k=(False, True),
     batch_heads="B*H <= 65535",
-    seq_len="N >= 1",
+    heads="H_kv divides H (grouped-query / multi-query K/V heads)",
+    seq_len="N >= 1, N_kv >= 1; N == N_kv when causal",
     return_lse=(False, True),
     attn_mask=False,
     smooth_v=False,
@@ -102,11 +103,16 @@ def _envelope_ok(q, k, v, tensor_layout, is_causal, sm_scale, return_lse, smooth
         return "head_dim"
     if q.size(0) != k.size(0) or q.size(0) != v.size(0):
         return "batch"
-    if q.size(1) != k.size(1) or q.size(1) != v.size(1):
+    # grouped K/V heads and a key length of its own, as the upstream API allows them
+    # (`sageattention/core.py:824-829` of the reference; its SK1 envelope refuses both,
+    # `sk1_backend/__init__.py:966-978`): H a multiple of H_kv, causal only with N == N_kv
+    if k.size(1) != v.size(1) or k.size(1) < 1 or q.size(1) % k.size(1) != 0:
         return "heads"
-    if q.size(2) != k.size(2) or k.size(2) != v.size(2):
+    if k.size(2) != v.size(2):
         return "seq_len"
-    if q.size(2) < 1:
+    if q.size(2) < 1 or k.size(2) < 1:
+        return "seq_len"
+    if is_causal and q.size(2) != k.size(2):
         return "seq_len"
     if q.size(0) * q.size(1) > 65535:
         return "batch_heads"
@@ -158,6 +164,8 @@ def try_sk1_t1(q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=None, 
 def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=None,
                 smooth_k=True, int8=None, events=None, kernel=0, return_lse=False):
     """The served path without the envelope check: allocate, prologue (2 launches), main loop.
+    q is (B, H, N, D) and k, v (B, H_kv, N_kv, D) in HND terms: query head h reads K/V head
+    h // (H // H_kv); N may differ from N_kv when not causal.
     `kernel` picks the main-loop kernel (0: by size, 1: 128 queries per block, 2: 256).
     With `return_lse`, returns `(out, lse)`: lse (B, H, N) fp32, each row's natural-log
     logsumexp of its scores times sm_scale (with smooth_k, corrected by sm_scale * q . mean_k, as
@@ -171,22 +179,24 @@ def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=
     else:
         qq, kk, vv = q, k, v
     B, H, N, D = (int(x) for x in qq.shape)
-    BH = B * H
+    H_kv, N_kv = int(kk.shape[1]), int(kk.shape[2])
+    BH_kv = B * H_kv
     is_bf16 = q.dtype == torch.bfloat16
     qk_int8 = (not is_bf16) and (int8 is None or bool(int8))
     sm = float(sm_scale if sm_scale is not None else D ** -0.5)
-    n_pad = n_pad_for(N)
+    n_pad = n_pad_for(N_kv)
     dev = q.device
-    k8 = torch.empty(BH, n_pad, D, device=dev,
+    # the prologue's outputs are per K/V plane: B*H_kv planes of N_kv keys
+    k8 = torch.empty(BH_kv, n_pad, D, device=dev,
                      dtype=torch.int8 if qk_int8 else torch.float8_e4m3fn)
-    sk = torch.empty(BH, n_pad, device=dev, dtype=torch.float32)
-    v8t = torch.empty(BH, D, n_pad, device=dev, dtype=torch.float8_e4m3fn)
-    sv = torch.empty(BH, n_pad, device=dev, dtype=torch.float32)
-    s = torch.empty(BH, device=dev, dtype=torch.float32)
-    kconst = torch.empty(BH, n_pad // 64, 3, 64, device=dev, dtype=torch.float32)
-    ws = torch.empty(lib.workspace_bytes(BH, N), device=dev, dtype=torch.uint8)
+    sk = torch.empty(BH_kv, n_pad, device=dev, dtype=torch.float32)
+    v8t = torch.empty(BH_kv, D, n_pad, device=dev, dtype=torch.float8_e4m3fn)
+    sv = torch.empty(BH_kv, n_pad, device=dev, dtype=torch.float32)
+    s = torch.empty(BH_kv, device=dev, dtype=torch.float32)
+    kconst = torch.empty(BH_kv, n_pad // 64, 3, 64, device=dev, dtype=torch.float32)
+    ws = torch.empty(lib.workspace_bytes(BH_kv, N_kv), device=dev, dtype=torch.uint8)
     lse = torch.empty(B, H, N, device=dev, dtype=torch.float32) if return_lse else None
-    kmean = (torch.empty(BH, D, device=dev, dtype=torch.float32)
+    kmean = (torch.empty(BH_kv, D, device=dev, dtype=torch.float32)
              if (return_lse and smooth_k) else None)
     if tensor_layout == "NHD":
         out = torch.empty(B, N, H, D, device=dev, dtype=q.dtype)
@@ -202,7 +212,7 @@ def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=
         if events is not None:
             events[1].record()
         lib.attn_fwd(qq, k8, kconst, v8t, s, oo, qk_int8=qk_int8, causal=bool(is_causal),
-                     sm_scale=sm, n_pad=n_pad, kernel=kernel, lse=lse, kmean=kmean)
+                     sm_scale=sm, n_pad=n_pad, kernel=kernel, lse=lse, kmean=kmean, n_kv=N_kv)
         if events is not None:
             events[2].record()
     return (out, lse) if return_lse else out

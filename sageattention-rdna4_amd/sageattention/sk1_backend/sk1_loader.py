@@ -111,7 +111,7 @@ class SageLib:
                                     + [vp, i64, i64, i64] + [i64] * 4 + [f32, vp])
         L.sage_attn_fwd_ex.restype = i32
         L.sage_attn_fwd_ex.argtypes = ([i32] * 3 + [vp, i64, i64, i64] + [vp] * 4
-                                       + [vp, i64, i64, i64] + [i64] * 4 + [f32, i32, vp, vp, vp])
+                                       + [vp, i64, i64, i64] + [i64] * 6 + [f32, i32, vp, vp, vp])
         L.sage_quant_q.restype = i32
         L.sage_quant_q.argtypes = [i32, i32, vp, i64, i64, i64, i64, i64, i64, f32, vp, vp, vp, vp]
         L.sage_mfma_layout_probe.restype = i32
@@ -145,18 +145,23 @@ class SageLib:
         self._check(rc, "sage_kv_prologue")
 
     def attn_fwd(self, q, k8, kconst, v8t, s, o, *, qk_int8, causal, sm_scale, n_pad, kernel=0,
-                 lse=None, kmean=None):
+                 lse=None, kmean=None, n_kv=None):
         """Main loop on logical (B, H, N, D) views `q`, `o` (see `sage_attn_fwd_ex`; `kernel`:
-        0 by size, 1 the 128-query kernel, 2 the 256-query ping-pong). `lse` (optional, (B, H, N)
-        fp32) receives each row's logsumexp; `kmean` ((B*H, 128) fp32) adds its smooth_k
-        correction."""
+        0 by size, 1 the 128-query kernel, 2 the 256-query ping-pong). The prologue outputs
+        `k8` (B*H_kv, n_pad, D) etc. give H_kv; `n_kv` is the key count (default N, and `n_pad`
+        is then ceil(n_kv/64)*64). `lse` (optional, (B, H, N) fp32) receives each row's
+        logsumexp; `kmean` ((B*H_kv, 128) fp32) adds its smooth_k correction."""
         B, H, N, _ = (int(x) for x in q.shape)
+        bh_kv = int(k8.shape[0])
+        if bh_kv % B:
+            raise ValueError("sage_attn_fwd: k8 holds %d planes, not a multiple of B=%d" % (bh_kv, B))
+        n_kv = N if n_kv is None else int(n_kv)
         rc = self.lib.sage_attn_fwd_ex(
             _dtype_code(q.dtype), int(bool(qk_int8)), int(bool(causal)),
             _ptr(q), q.stride(0), q.stride(1), q.stride(2),
             _ptr(k8), _ptr(kconst), _ptr(v8t), _ptr(s),
             _ptr(o), o.stride(0), o.stride(1), o.stride(2),
-            B, H, N, int(n_pad), ctypes.c_float(float(sm_scale)), int(kernel),
+            B, H, N, bh_kv // B, n_kv, int(n_pad), ctypes.c_float(float(sm_scale)), int(kernel),
             _ptr(lse), _ptr(kmean), ctypes.c_void_p(torch_stream(q.device)))
         self._check(rc, "sage_attn_fwd")
 

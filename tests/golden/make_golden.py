@@ -27,11 +27,16 @@ import oracle  # noqa: E402
 from sage_testutil import make_qkv  # noqa: E402
 
 CASES = {
-    # name: (dtype, B, H, N, causal, smooth_k, layout, std, k_offset, outliers, seed)
+    # name: (dtype, B, H, N, causal, smooth_k, layout, std, k_offset, outliers, seed[, H_kv, N_kv])
     "fp16_n77_causal": (torch.float16, 1, 1, 77, True, True, "HND", 1.0, 2.0, 0.03, 11),
     "fp16_n1_noncausal": (torch.float16, 1, 2, 1, False, True, "HND", 1.0, 2.0, 0.0, 12),
     "fp16_n70_nhd_nosmooth": (torch.float16, 2, 1, 70, False, False, "NHD", 1.0, 0.0, 0.0, 13),
     "bf16_n67_causal": (torch.bfloat16, 1, 1, 67, True, True, "HND", 1.5, 2.0, 0.02, 14),
+    # grouped K/V heads with a longer key sequence; one shared K/V head with a shorter one
+    "fp16_gqa_h4kv2_n70_kv130": (torch.float16, 1, 4, 70, False, True, "HND", 1.0, 2.0, 0.02, 15,
+                                 2, 130),
+    "bf16_mqa_nhd_n100_kv37": (torch.bfloat16, 2, 3, 100, False, True, "NHD", 1.0, 1.0, 0.0, 16,
+                               1, 37),
 }
 
 
@@ -57,14 +62,16 @@ def corner_rows(q, k, v, layout):
 
 
 def make(name):
-    dtype, B, H, N, causal, smooth_k, layout, std, off, outl, seed = CASES[name]
+    dtype, B, H, N, causal, smooth_k, layout, std, off, outl, seed = CASES[name][:11]
+    H_kv, N_kv = CASES[name][11:] or (H, N)
     q, k, v = make_qkv(B, H, N, seed=seed, dtype=dtype, layout=layout, std=std, k_offset_std=off,
-                       outlier_frac=outl)
+                       outlier_frac=outl, h_kv=H_kv, n_kv=N_kv)
     q, k, v = corner_rows(q, k, v, layout)
     r = oracle.emulate_sageattn(q, k, v, tensor_layout=layout, is_causal=causal, smooth_k=smooth_k)
     arr = dict(
+        # B, H, N, causal, smooth_k, NHD, bf16, H_kv, N_kv
         meta=np.array([B, H, N, int(causal), int(smooth_k), int(layout == "NHD"),
-                       int(dtype == torch.bfloat16)], dtype=np.int64),
+                       int(dtype == torch.bfloat16), H_kv, N_kv], dtype=np.int64),
         sm_scale=np.array([r["sm_scale"]], dtype=np.float32),
         q=bits(q), k=bits(k), v=bits(v),
         k8=bits(r["k8"]) if r["k8"].dtype != torch.int8 else r["k8"].numpy(),

@@ -15,25 +15,29 @@ def have_gfx950():
 
 
 def make_qkv(b, h, n, *, seed=0, dtype=torch.float16, layout="HND", std=1.0, k_offset_std=0.0,
-             outlier_frac=0.0, outlier_scale=50.0, d=HEAD_DIM):
+             outlier_frac=0.0, outlier_scale=50.0, d=HEAD_DIM, h_kv=None, n_kv=None):
     """Seeded CPU tensors, cast to `dtype` (the GPU and the oracle then see identical bytes).
 
     Q, K, V ~ N(0, std). K gets a per-(b,h) channel offset mu ~ N(0, k_offset_std) broadcast over
-    tokens, and `round(outlier_frac * n)` K rows per plane (seeded choice) are scaled by
-    `outlier_scale` -- the synthetic inputs of the benchmark configurations.
+    tokens, and `round(outlier_frac * n_kv)` K rows per plane (seeded choice) are scaled by
+    `outlier_scale` -- the synthetic inputs of the benchmark configurations. K and V have `h_kv`
+    heads and `n_kv` rows (default h and n; with the defaults the draws are the same as before
+    these parameters existed).
     Returns (q, k, v) in `layout` ("HND" (B,H,N,D) or "NHD" (B,N,H,D)), contiguous.
     """
+    hk = h if h_kv is None else h_kv
+    nk = n if n_kv is None else n_kv
     g = torch.Generator().manual_seed(seed)
     q = torch.randn(b, h, n, d, generator=g) * std
-    k = torch.randn(b, h, n, d, generator=g) * std
-    v = torch.randn(b, h, n, d, generator=g) * std
+    k = torch.randn(b, hk, nk, d, generator=g) * std
+    v = torch.randn(b, hk, nk, d, generator=g) * std
     if k_offset_std:
-        k = k + torch.randn(b, h, 1, d, generator=g) * k_offset_std
-    n_out = int(round(outlier_frac * n))
+        k = k + torch.randn(b, hk, 1, d, generator=g) * k_offset_std
+    n_out = int(round(outlier_frac * nk))
     if n_out:
         for bi in range(b):
-            for hi in range(h):
-                idx = torch.randperm(n, generator=g)[:n_out]
+            for hi in range(hk):
+                idx = torch.randperm(nk, generator=g)[:n_out]
                 k[bi, hi, idx] *= outlier_scale
     out = [t.to(dtype) for t in (q, k, v)]
     if layout == "NHD":

@@ -64,14 +64,19 @@ def test_library_host_calls_without_a_gpu():
                              ctypes.c_void_p(16), 8, 8, 8, 1, 1, 100, 96, ctypes.c_float(0.1), None)
     assert rc == 1 and b"n_pad" in L.lib.sage_last_error()
     p16 = ctypes.c_void_p(16)
-    rc = L.lib.sage_attn_fwd_ex(0, 1, 0, p16, 12800, 12800, 128, p16, p16, p16, p16,
-                                p16, 12800, 12800, 128, 1, 1, 100, 128, ctypes.c_float(0.1), 7,
-                                None, None, None)
-    assert rc == 1 and b"kernel" in L.lib.sage_last_error()
-    rc = L.lib.sage_attn_fwd_ex(0, 1, 0, p16, 12800, 12800, 128, p16, p16, p16, p16,
-                                p16, 12800, 12800, 128, 1, 1, 100, 128, ctypes.c_float(0.1), 0,
-                                ctypes.c_void_p(18), None, None)
-    assert rc == 1 and b"lse must be 4-byte aligned" in L.lib.sage_last_error()
+    def ex(causal=0, H=1, N=100, H_kv=1, N_kv=100, N_kv_pad=128, kernel=0, lse=None):
+        return L.lib.sage_attn_fwd_ex(0, 1, causal, p16, 12800, 12800, 128, p16, p16, p16, p16,
+                                      p16, 12800, 12800, 128, 1, H, N, H_kv, N_kv, N_kv_pad,
+                                      ctypes.c_float(0.1), kernel, lse, None, None)
+    assert ex(kernel=7) == 1 and b"kernel" in L.lib.sage_last_error()
+    assert ex(lse=ctypes.c_void_p(18)) == 1
+    assert b"lse must be 4-byte aligned" in L.lib.sage_last_error()
+    # grouped K/V heads: H must be a multiple of H_kv; causal needs N == N_kv
+    assert ex(H=6, H_kv=4) == 1 and b"heads" in L.lib.sage_last_error()
+    assert ex(H=1, H_kv=0) == 1 and b"heads" in L.lib.sage_last_error()
+    assert ex(causal=1, N_kv=99) == 1 and b"seq_len" in L.lib.sage_last_error()
+    assert ex(N_kv=200, N_kv_pad=192) == 1 and b"n_pad" in L.lib.sage_last_error()
+    assert ex(N_kv=0, N_kv_pad=64) == 1 and b"n_lt_1" in L.lib.sage_last_error()
 
 
 def test_strided_view_reason_rule():

@@ -416,3 +416,76 @@ def test_nhd_layout_is_a_view():
     qn, kn, vn = (t.transpose(1, 2).contiguous() for t in (q, k, v))
     b = oracle.emulate_sageattn(qn, kn, vn, tensor_layout="NHD", is_causal=True)["o"]
     assert torch.equal(b.transpose(1, 2), a)
+
+
+# ----------------------------------------------------------------------------- GQA, kv length
+def test_exact_attention_gqa_and_kv_length_match_torch_sdpa():
+    # The yardstick's head map and key length against torch's own SDPA (enable_gqa repeats each
+    # K/V head over its group of H // H_kv query heads), fp64 on the CPU.
+    sdpa = torch.nn.functional.scaled_dot_product_attention
+    for (h, hk, n, nk, causal) in ((6, 2, 40, 40, True), (6, 3, 17, 90, False), (4, 1, 70, 9, False)):
+        q, k, v = make_qkv(2, h, n, seed=h + nk, h_kv=hk, n_kv=nk)
+        want = sdpa(q.double(), k.double(), v.double(), is_causal=causal, enable_gqa=True)
+        got = oracle.exact_attention(q, k, v, is_causal=causal)
+        assert torch.allclose(got, want, rtol=1e-10, atol=1e-12)
+        s = torch.matmul(q.double(), k.double().repeat_interleave(h // hk, 1).transpose(2, 3))
+        s = s * q.shape[-1] ** -0.5
+        if causal:
+            s = s.masked_fill(torch.ones(n, nk, dtype=torch.bool).triu(1), -math.inf)
+        assert torch.allclose(oracle.exact_lse(q, k, is_causal=causal), torch.logsumexp(s, -1))
+
+
+def test_gqa_equals_repeated_kv_heads():
+    # Grouped K/V heads are, by definition, each K/V head repeated over its group: the emulation
+    # with H_kv heads must give the bits of the emulation on explicitly repeated K/V (per-token
+    # quantization, the per-plane mean and the per-plane fold are all unchanged by the repeat).
+    for dtype in (torch.float16, torch.bfloat16):
+        q, k, v = make_qkv(2, 6, 100, seed=8, dtype=dtype, h_kv=2, k_offset_std=1.5)
+        a = oracle.emulate_sageattn(q, k, v, is_causal=True)
+        b = oracle.emulate_sageattn(q, k.repeat_interleave(3, 1), v.repeat_interleave(3, 1),
+                                    is_causal=True)
+        assert torch.equal(a["o"], b["o"]) and torch.equal(a["lse"], b["lse"])
+        assert a["k8"].shape[0] == 4 and b["k8"].shape[0] == 12
+        # the map matters: heads of different groups see different K/V
+        assert not torch.equal(a["o"][:, 0], a["o"][:, 3])
+
+
+def test_kv_plane_map_and_refusals():
+    assert oracle.kv_planes(2, 6, 2, 5, 5, True).tolist() == [0, 0, 0, 1, 1, 1, 2, 2, 2, 3, 3, 3]
+    assert oracle.kv_planes(1, 4, 4, 5, 9, False).tolist() == [0, 1, 2, 3]
+    assert oracle.kv_planes(1, 4, 1, 5, 9, False).tolist() == [0, 0, 0, 0]
+    with pytest.raises(ValueError):
+        oracle.kv_planes(1, 6, 4, 5, 5, False)
+    with pytest.raises(ValueError):
+        oracle.kv_planes(1, 4, 4, 5, 9, True)
+
+
+@pytest.mark.parametrize("nq,nk", [(5, 130), (130, 5), (64, 200)])
+def test_kv_length_rows_are_independent_of_q_length(nq, nk):
+    # With its own key length, each query row sees all N_kv keys: the emulation of a few rows
+    # equals those rows of a longer call on the same K/V (a key mask taken from the query length
+    # would drop or invent keys), and every row matches the brute-force restatement.
+    q, k, v = make_qkv(1, 1, max(nq, 140), seed=nq + nk, n_kv=nk, k_offset_std=1.0)
+    full = oracle.emulate_sageattn(q, k, v)
+    part = oracle.emulate_sageattn(q[:, :, :nq], k, v)
+    assert torch.equal(part["o"], full["o"][:, :, :nq])
+    assert torch.equal(part["lse"], full["lse"][:, :, :nq])
+    r = part
+    k8 = r["k8"][0].numpy().astype(np.int32)
+    v8t = r["v8t"][0].float().numpy()
+    q8 = r["q8"][0].numpy().astype(np.int32)
+    out = r["o"][0, 0].float().numpy()
+    for row in sorted({0, nq // 2, nq - 1}):
+        want = _brute_force_row(q8[row], r["c_q"][0, row].item(), k8, r["sk"][0].numpy(), v8t,
+                                r["svp"][0].numpy(), r["s"][0].item(), row, nk, False, True)
+        assert np.allclose(out[row], want.astype(np.float16).astype(np.float32), rtol=2e-3,
+                           atol=2e-4), row
+
+
+def test_gqa_and_kv_length_close_to_exact_attention():
+    for dtype in (torch.float16, torch.bfloat16):
+        q, k, v = make_qkv(1, 8, 300, seed=2, dtype=dtype, h_kv=2, n_kv=515)
+        o = oracle.emulate_sageattn(q, k, v)["o"].double()
+        ex = oracle.exact_attention(q, k, v)
+        rel = ((o - ex).pow(2).mean().sqrt() / ex.pow(2).mean().sqrt()).item()
+        assert rel < 0.08, (dtype, rel)
