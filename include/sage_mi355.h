@@ -64,21 +64,30 @@ size_t sage_kv_prologue_workspace_bytes(int64_t BH, int64_t N);
  *   dtype     SAGE_F16 or SAGE_BF16 (K and V share it)
  *   k_int8    1: K to int8 (fp16 only); 0: K to fp8 e4m3
  *   smooth_k  1: subtract the sequence mean of K first
+ *   smooth_v  1: subtract the sequence mean of V (fp64-accumulated, rounded once to fp32, written
+ *             to `vmean`) before V's per-token scale and quantization; the main loop adds it back
+ *             (sage_attn_fwd_ex's `vmean`). The reference's Triton quantizer's SUB_VMEAN path
+ *             (`sageattention/sk1_backend/quant_triton.py:668-678`, `:714-717`) with the
+ *             VMEAN epilogue of `kernels/hip/sk1_t6i.hip:290-297`; its shipped HIP prologue
+ *             does not produce the mean (`sageattention/sk1_backend/hip_prologue.py:17`).
+ *             Costs a third launch (V is read twice).
  *   fold      1: write SV' = SV / S into `sv`; 0: leave SV unfolded (S is written either way)
  *   k, v      logical (B, H, N, 128) views with element strides (k_sb, k_sh, k_sr) / (v_...)
  *   outputs   k8, sk, v8t, sv, s (required); mean (may be NULL; written when smooth_k);
+ *             vmean (B*H, 128) fp32 (required with smooth_v, else unused);
  *             kconst (may be NULL): the main loop's per-key constants, (B*H, N_pad/64, 3, 64) fp32:
  *             for each 64-key block SK, the fma addend -RN(1.5*2^23*SK) (0 when !k_int8) and
  *             RN(SV'*448) -- a layout of SK and SV' (no reference counterpart: the reference's
  *             kernel derives them from SK/SV itself, `kernels/hip/sk1_t6i.hip:189-207`, `:249-262`)
  *   workspace at least sage_kv_prologue_workspace_bytes(B*H, N) bytes, 256-byte aligned
  */
-int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int fold,
+int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int smooth_v, int fold,
                      const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sr,
                      const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sr,
                      int64_t B, int64_t H, int64_t N, int64_t N_pad,
-                     void* k8, float* sk, void* v8t, float* sv, float* mean, float* s,
-                     float* kconst, void* workspace, size_t workspace_bytes, void* stream);
+                     void* k8, float* sk, void* v8t, float* sv, float* mean, float* vmean,
+                     float* s, float* kconst, void* workspace, size_t workspace_bytes,
+                     void* stream);
 
 /*
  * The quantized flash-attention main loop (one launch on `stream`).
@@ -124,6 +133,10 @@ int sage_attn_fwd(int dtype, int qk_int8, int causal,
  *          return_lse (`sageattention/sk1_backend/__init__.py:925-926`); this fills that row.
  *   kmean  optional (B*H_kv, 128) fp32: the smooth_k mean the prologue subtracted (its `mean`
  *          output); used only with lse.
+ *   vmean  optional (B*H_kv, 128) fp32: the smooth_v mean the prologue subtracted from V (its
+ *          `vmean` output); each output element is then T(fma(acc, S/(l*448), vmean[d])), the
+ *          reference's epilogue `acc * inv + vm` (`kernels/hip/sk1_t6i.hip:290-297`). NULL: no
+ *          add-back.
  */
 int sage_attn_fwd_ex(int dtype, int qk_int8, int causal,
                      const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sr,
@@ -131,7 +144,7 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal,
                      void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr,
                      int64_t B, int64_t H, int64_t N, int64_t H_kv, int64_t N_kv,
                      int64_t N_kv_pad, float sm_scale, int kernel,
-                     float* lse, const float* kmean, void* stream);
+                     float* lse, const float* kmean, const float* vmean, void* stream);
 
 /*
  * Q quantization exactly as the main loop performs it, written out for parity checks.

@@ -103,16 +103,21 @@ def quant_k(k, n_pad, mean=None, int8=True):
     return k8, sk
 
 
-def quant_v(v, n_pad):
+def quant_v(v, n_pad, mean=None):
     """V per-token fp8 quantization, stored transposed (`kernels/hip/h34_prologue.hip:168-211`).
 
     `vmax = max_d |v|`; `sv = max(RN(vmax / 448), 1e-12)`; `SV = sv` on live rows, `0.0` on pad rows
     (`h34_prologue.hip:186`); `V8T[d, n] = e4m3(min(RN(v[n, d] / sv), 448))`, 0 on pad rows.
+    With `mean` (smooth_v), `v` is first `RN(fp32(v) - mean)` on live rows, before the absmax
+    (`sageattention/sk1_backend/quant_triton.py:714-719`); pad rows stay 0.
 
     Returns `(V8T (BH, D, n_pad) float8_e4m3fn, SV (BH, n_pad) fp32)`.
     """
     BH, N, D = v.shape
-    vf = _pad_rows(v, n_pad)
+    vf = v.to(torch.float32)
+    if mean is not None:
+        vf = vf - mean[:, None, :].to(torch.float32)
+    vf = _pad_rows(vf, n_pad)
     vmax = vf.abs().amax(dim=2)
     sv = torch.maximum(vmax / P_SCALE, FLOOR)
     x = torch.minimum(vf / sv[:, :, None], P_SCALE)
@@ -160,7 +165,7 @@ def quant_q(q, sm_scale, int8=True):
 
 
 def attention_tiles(q8, c_q, k8, sk, v8t, svp, s_fold, N, causal, out_dtype, tile=BN,
-                    q_chunk=2048, row0=0, lse_out=None):
+                    q_chunk=2048, row0=0, lse_out=None, vmean=None):
     """The main loop's online softmax over key tiles, in the reference's phase order.
 
     Follows `kernels/hip/sk1_t6i.hip:162-299` (and the identical fp8 form of `sk1_t4a1s.hip`):
@@ -170,7 +175,10 @@ def attention_tiles(q8, c_q, k8, sk, v8t, svp, s_fold, N, causal, out_dtype, til
     * `m_new = max(m, max_tile s)`; `m_use = m_new`, or 0 when it is -inf; `alpha = exp2(m - m_use)`;
     * `p = exp2(s - m_use)`; `l = l*alpha + sum_tile p` (the row sum is taken before the fold);
     * `p8 = e4m3(RN(p * RN(SV'[n] * 448)))`; `acc = acc*alpha + sum_n p8 * V8[n]` in fp32;
-    and the epilogue `O = T(acc * (l > 0 ? RN(S / RN(l * 448)) : 0))` (`sk1_t6i.hip:281-299`).
+    and the epilogue `O = T(acc * (l > 0 ? RN(S / RN(l * 448)) : 0))` (`sk1_t6i.hip:281-299`), or
+    with `vmean` ((BH, D) fp32, smooth_v) `O = T(fma(acc, inv, vmean[d]))`, the kernel's
+    `acc * inv + vm` (`sk1_t6i.hip:290-297`), evaluated in fp64 (where acc*inv is exact) and
+    rounded to fp32.
 
     The GPU uses the hardware `exp2` and an unspecified MFMA accumulation order, so the output is
     pinned by tolerance, not bits. Queries are processed in chunks of `q_chunk` rows to bound
@@ -218,7 +226,11 @@ def attention_tiles(q8, c_q, k8, sk, v8t, svp, s_fold, N, causal, out_dtype, til
             acc = acc * alpha[:, :, None] + torch.matmul(p8, vf[:, :, ks].transpose(1, 2))
             m = m_new
         inv = torch.where(l > 0, s_fold[:, None] / (l * P_SCALE), torch.zeros_like(l))
-        out[:, r0:r1] = (acc * inv[:, :, None]).to(out_dtype)
+        if vmean is None:
+            out[:, r0:r1] = (acc * inv[:, :, None]).to(out_dtype)
+        else:
+            o64 = acc.double() * inv.double()[:, :, None] + vmean.double()[:, None, :]
+            out[:, r0:r1] = o64.to(torch.float32).to(out_dtype)
         if lse_out is not None:
             m_use = torch.where(m == -math.inf, torch.zeros_like(m), m)
             lse_out[:, r0:r1] = m_use + torch.log2(l)
@@ -255,7 +267,7 @@ def kv_planes(B, H, H_kv, N, N_kv, is_causal):
 
 
 def emulate_sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=None, smooth_k=True,
-                     qk_int8=None):
+                     qk_int8=None, smooth_v=False):
     """The whole SK1 call on the CPU, returning every intermediate.
 
     Routing follows `sageattention/sk1_backend/__init__.py:1161-1272`: fp16 inputs use int8 Q.K
@@ -263,11 +275,14 @@ def emulate_sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=Non
     fp16 inputs. `sm_scale` defaults to `D ** -0.5` (`__init__.py:1165`).
 
     k and v may have H_kv heads (H a multiple of H_kv) and N_kv rows (N_kv == N when causal):
-    query plane b*H + h reads K/V plane `kv_planes(...)[b*H + h]`.
+    query plane b*H + h reads K/V plane `kv_planes(...)[b*H + h]`. `smooth_v` subtracts V's
+    sequence mean (the same fp64-accumulated mean as K's) before quantizing V and adds it back in
+    the epilogue (`quant_triton.py:668-678` of the reference; its shipped HIP prologue does not
+    compute V's mean).
 
-    Returns a dict with `mean, k8, sk, v8t, sv, s, svp, q8, sq, c_q, o, lse` where `o` has the
+    Returns a dict with `mean, vmean, k8, sk, v8t, sv, s, svp, q8, sq, c_q, o, lse` where `o` has the
     caller's layout and dtype, `lse` is (B, H, N) fp32 (the `return_lse` output), `q8, sq, c_q`
-    are per query plane (B*H, ...) and `mean, k8, sk, v8t, sv, s, svp` per K/V plane
+    are per query plane (B*H, ...) and `mean, vmean, k8, sk, v8t, sv, s, svp` per K/V plane
     (B*H_kv, ...).
     """
     qq, kk, vv = (to_hnd(t, tensor_layout) for t in (q, k, v))
@@ -283,17 +298,19 @@ def emulate_sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=Non
     kr, vr = (t.reshape(B * H_kv, N_kv, D) for t in (kk, vv))
     mean = kseq_mean(kr) if smooth_k else None
     k8, sk = quant_k(kr, n_pad, mean=mean, int8=qk_int8)
-    v8t, sv = quant_v(vr, n_pad)
+    vmean = kseq_mean(vr) if smooth_v else None
+    v8t, sv = quant_v(vr, n_pad, mean=vmean)
     s, svp = fold_v_scale(sv)
     q8, sq, c_q = quant_q(qr, sm, int8=qk_int8)
     lse2 = torch.empty(BH, N, dtype=torch.float32)
     o = attention_tiles(q8, c_q, k8[kvp], sk[kvp], v8t[kvp], svp[kvp], s[kvp], N_kv, is_causal,
-                        q.dtype, lse_out=lse2)
+                        q.dtype, lse_out=lse2, vmean=None if vmean is None else vmean[kvp])
     o = o.view(B, H, N, D)
     if tensor_layout == "NHD":
         o = o.transpose(1, 2).contiguous()
     lse = row_lse(lse2, qr, None if mean is None else mean[kvp], sm).view(B, H, N)
-    return dict(mean=mean, k8=k8, sk=sk, v8t=v8t, sv=sv, s=s, svp=svp, q8=q8, sq=sq, c_q=c_q, o=o,
+    return dict(mean=mean, vmean=vmean, k8=k8, sk=sk, v8t=v8t, sv=sv, s=s, svp=svp, q8=q8, sq=sq,
+                c_q=c_q, o=o,
                 lse=lse, n_pad=n_pad, sm_scale=sm)
 
 

@@ -42,7 +42,8 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
     const u8* __restrict__ V8T, const float* __restrict__ Sfold,
     T* __restrict__ O, int64_t q_sb, int64_t q_sh, int64_t q_sr, int64_t o_sb, int64_t o_sh,
     int64_t o_sr, int H, int H_kv, int G, int N, int Nk, int Nk_pad, int num_qt, int xcd_span,
-    float sm_scale, float* __restrict__ LSE, const float* __restrict__ KMEAN) {
+    float sm_scale, float* __restrict__ LSE, const float* __restrict__ KMEAN,
+    const float* __restrict__ VMEAN) {
   // Three staging buffers (K tile, V^T tile, per-key constants), declared as separate objects:
   // with the buffer chosen at compile time the compiler can tell a DMA into one buffer from reads
   // of another, and waits for a DMA only where its own buffer is read. (Its wait bookkeeping
@@ -189,19 +190,28 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) asm volatile("" ::"v"(acc[dt]));
 
-  // ---------- epilogue: O = acc * S / (l * 448) ----------
+  // ---------- epilogue: O = acc * S / (l * 448) (+ V's mean with smooth_v, one fma) ----------
   if (qrow < N) {
     if (LSE && hh == 0) LSE[(int64_t)bh * N + qrow] = row_lse(mc, l_i, sm_scale, qmu);
     const float inv = (l_i > 0.0f) ? __fdiv_rn(Sb, l_i * P_SCALE) : 0.0f;
     T* op = O + b * o_sb + hd * o_sh + (int64_t)qrow * o_sr;
+    const float* vmp = VMEAN ? VMEAN + (int64_t)kvp * HD : nullptr;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d = 32 * dt + 8 * g + 4 * hh;
         T ov[4];
+        if (vmp) {
+          const float4 vm = *(const float4*)(vmp + d);
+          ov[0] = (T)__builtin_fmaf(acc[dt][4 * g + 0], inv, vm.x);
+          ov[1] = (T)__builtin_fmaf(acc[dt][4 * g + 1], inv, vm.y);
+          ov[2] = (T)__builtin_fmaf(acc[dt][4 * g + 2], inv, vm.z);
+          ov[3] = (T)__builtin_fmaf(acc[dt][4 * g + 3], inv, vm.w);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ov[e] = (T)(acc[dt][4 * g + e] * inv);
+          for (int e = 0; e < 4; ++e) ov[e] = (T)(acc[dt][4 * g + e] * inv);
+        }
         uint2 packed;
         __builtin_memcpy(&packed, ov, 8);
         *(uint2*)(op + d) = packed;
@@ -287,7 +297,7 @@ static void launch_attn_t(const AttnArgs& a, hipStream_t stream) {
                      (const T*)a.q, (const u8*)a.k8, a.kconst, (const u8*)a.v8t, a.s, (T*)a.o,
                      a.q_sb, a.q_sh, a.q_sr, a.o_sb, a.o_sh, a.o_sr, (int)a.H, (int)a.H_kv,
                      (int)(a.H / a.H_kv), (int)a.N, (int)a.N_kv, (int)a.N_kv_pad, num_qt, span,
-                     a.sm_scale, a.lse, a.kmean);
+                     a.sm_scale, a.lse, a.kmean, a.vmean);
 }
 
 hipError_t launch_attn_fwd(const AttnArgs& a, hipStream_t stream) {

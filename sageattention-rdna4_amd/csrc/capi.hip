@@ -74,11 +74,12 @@ size_t sage_kv_prologue_workspace_bytes(int64_t BH, int64_t N) {
   return sage::prologue_workspace_bytes(BH, (N + 63) / 64 * 64);
 }
 
-int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int fold, const void* k, int64_t k_sb,
-                     int64_t k_sh, int64_t k_sr, const void* v, int64_t v_sb, int64_t v_sh,
-                     int64_t v_sr, int64_t B, int64_t H, int64_t N, int64_t N_pad, void* k8,
-                     float* sk, void* v8t, float* sv, float* mean, float* s, float* kconst,
-                     void* workspace, size_t workspace_bytes, void* stream) {
+int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int smooth_v, int fold, const void* k,
+                     int64_t k_sb, int64_t k_sh, int64_t k_sr, const void* v, int64_t v_sb,
+                     int64_t v_sh, int64_t v_sr, int64_t B, int64_t H, int64_t N, int64_t N_pad,
+                     void* k8, float* sk, void* v8t, float* sv, float* mean, float* vmean,
+                     float* s, float* kconst, void* workspace, size_t workspace_bytes,
+                     void* stream) {
   if (dtype != SAGE_F16 && dtype != SAGE_BF16)
     return fail(SAGE_ERR_INVALID, "dtype: unsupported dtype code %d", dtype);
   if (dtype == SAGE_BF16 && k_int8)
@@ -88,6 +89,8 @@ int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int fold, const void* 
   if ((rc = check_view("k", k, k_sb, k_sh, k_sr))) return rc;
   if ((rc = check_view("v", v, v_sb, v_sh, v_sr))) return rc;
   if (!k8 || !sk || !v8t || !sv || !s) return fail(SAGE_ERR_INVALID, "an output pointer is NULL");
+  if (smooth_v && !vmean)
+    return fail(SAGE_ERR_INVALID, "vmean: smooth_v needs the vmean output (B*H x 128 fp32)");
   if (!aligned16(k8) || !aligned16(v8t) || !aligned16(sk) || !aligned16(sv) || !aligned16(kconst))
     return fail(SAGE_ERR_INVALID, "ptr_align: outputs must be 16-byte aligned");
   const size_t need = sage::prologue_workspace_bytes(B * H, N_pad);
@@ -98,6 +101,7 @@ int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int fold, const void* 
   a.dtype = dtype;
   a.k_int8 = k_int8 ? 1 : 0;
   a.smooth_k = smooth_k ? 1 : 0;
+  a.smooth_v = smooth_v ? 1 : 0;
   a.fold = fold ? 1 : 0;
   a.k = k;
   a.k_sb = k_sb;
@@ -116,6 +120,7 @@ int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int fold, const void* 
   a.v8t = v8t;
   a.sv = sv;
   a.mean = smooth_k ? mean : nullptr;
+  a.vmean = smooth_v ? vmean : nullptr;
   a.s = s;
   a.kconst = kconst;
   a.workspace = workspace;
@@ -127,7 +132,7 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
                      const void* v8t, const float* s, void* o, int64_t o_sb, int64_t o_sh,
                      int64_t o_sr, int64_t B, int64_t H, int64_t N, int64_t H_kv, int64_t N_kv,
                      int64_t N_kv_pad, float sm_scale, int kernel, float* lse,
-                     const float* kmean, void* stream) {
+                     const float* kmean, const float* vmean, void* stream) {
   if (dtype != SAGE_F16 && dtype != SAGE_BF16)
     return fail(SAGE_ERR_INVALID, "dtype: unsupported dtype code %d", dtype);
   if (dtype == SAGE_BF16 && qk_int8)
@@ -154,6 +159,8 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
     return fail(SAGE_ERR_INVALID, "ptr_align: lse must be 4-byte aligned");
   if (kmean && !aligned16(kmean))
     return fail(SAGE_ERR_INVALID, "ptr_align: kmean must be 16-byte aligned");
+  if (vmean && !aligned16(vmean))
+    return fail(SAGE_ERR_INVALID, "ptr_align: vmean must be 16-byte aligned");
   sage::AttnArgs a;
   a.dtype = dtype;
   a.qk_int8 = qk_int8 ? 1 : 0;
@@ -179,6 +186,7 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
   a.sm_scale = sm_scale;
   a.lse = lse;
   a.kmean = lse ? kmean : nullptr;
+  a.vmean = vmean;
   // The 256-query ping-pong pays off on long sequences; at short ones its larger tiles leave too
   // few blocks per CU and more causal diagonal work, and the 128-query kernel is as fast or faster.
   const bool q256 = kernel == SAGE_KERNEL_Q256 ||
@@ -194,7 +202,7 @@ int sage_attn_fwd(int dtype, int qk_int8, int causal, const void* q, int64_t q_s
                   int64_t H, int64_t N, int64_t N_pad, float sm_scale, void* stream) {
   return sage_attn_fwd_ex(dtype, qk_int8, causal, q, q_sb, q_sh, q_sr, k8, kconst, v8t, s, o,
                           o_sb, o_sh, o_sr, B, H, N, H, N, N_pad, sm_scale, SAGE_KERNEL_AUTO,
-                          nullptr, nullptr, stream);
+                          nullptr, nullptr, nullptr, stream);
 }
 
 int sage_quant_q(int dtype, int qk_int8, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sr,

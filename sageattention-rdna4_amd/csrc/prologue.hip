@@ -1,6 +1,6 @@
 // The K/V prologue on gfx950: two launches, both HBM-bound streaming passes.
 //
-//   1. stats pass  (kv_stats_kernel):  reads K and V once.
+//   1. stats pass  (kv_stats_kernel):  reads K and V once (with smooth_v: twice, see VMode).
 //        * K: per-column fp64 partial sums over the block's rows (the smooth_k mean), written to the
 //          workspace as C1 partials per plane -- no atomics, so the sum order is fixed;
 //        * V: per-token scale sv = max(RN(vmax/448), 1e-12), e4m3 quantization, and the transposed
@@ -42,11 +42,16 @@ PrologueGeom prologue_geom(int64_t BH, int64_t N_pad) {
   return g;
 }
 
+// Workspace: K's mean partials, V's mean partials (smooth_v), the per-block max of sv -- each
+// region 256-byte aligned. The V region is always reserved, so the size does not depend on flags.
+static size_t part_region_bytes(int64_t BH, const PrologueGeom& g) {
+  return ((size_t)BH * g.C1 * HD * sizeof(double) + 255) / 256 * 256;
+}
+
 size_t prologue_workspace_bytes(int64_t BH, int64_t N_pad) {
   const PrologueGeom g = prologue_geom(BH, N_pad);
-  const size_t part = (size_t)BH * g.C1 * HD * sizeof(double);
   const size_t smax = (size_t)BH * g.C1 * sizeof(float);
-  return ((part + 255) / 256 * 256) + ((smax + 255) / 256 * 256);
+  return 2 * part_region_bytes(BH, g) + ((smax + 255) / 256 * 256);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -56,14 +61,22 @@ size_t prologue_workspace_bytes(int64_t BH, int64_t N_pad) {
 // tile is [128 d][144 B]; the 8-byte chunk of tokens 8rg..8rg+7 of row d sits at chunk position
 // rg ^ (d >> 3), which keeps both the column writes and the row reads free of bank conflicts.
 // ---------------------------------------------------------------------------------------------
-template <typename T>
+// V_QUANT: V quantized as it is (and K's mean partials when smooth_k) -- the whole stats pass.
+// V_SUMS: K's and V's mean partials only (smooth_v, first launch).
+// V_CENTERED: V's mean from its partials (written to VMEAN), V - mean quantized (smooth_v, second
+//             launch; K is not read).
+enum VMode { V_QUANT = 0, V_SUMS = 1, V_CENTERED = 2 };
+
+template <typename T, int VMODE>
 __global__ __launch_bounds__(PT) void kv_stats_kernel(
     const T* __restrict__ K, const T* __restrict__ V, u8* __restrict__ V8T, float* __restrict__ SV,
-    double* __restrict__ part, float* __restrict__ smax, int64_t H, int64_t N, int64_t N_pad,
-    int64_t R1, int64_t C1, int64_t k_sb, int64_t k_sh, int64_t k_sr, int64_t v_sb, int64_t v_sh,
-    int64_t v_sr, int smooth_k) {
+    double* __restrict__ part, double* __restrict__ vpart, float* __restrict__ VMEAN,
+    float* __restrict__ smax, int64_t H, int64_t N, int64_t N_pad, int64_t R1, int64_t C1,
+    int64_t k_sb, int64_t k_sh, int64_t k_sr, int64_t v_sb, int64_t v_sh, int64_t v_sr,
+    int smooth_k) {
   __shared__ __attribute__((aligned(16))) u8 tile[HD * VT_STRIDE];
   __shared__ float wmax[PT / 64];
+  __shared__ float vmu_s[HD];
 
   const int tid = threadIdx.x, cg = tid & 15, rg = tid >> 4;
   const int64_t c = blockIdx.x, bh = blockIdx.y;
@@ -73,10 +86,27 @@ __global__ __launch_bounds__(PT) void kv_stats_kernel(
   u8* vt = V8T + bh * HD * N_pad;
   const int64_t r_begin = c * R1;
   const int64_t r_end = (r_begin + R1 < N_pad) ? r_begin + R1 : N_pad;
+  const bool k_sums = smooth_k && VMODE != V_CENTERED;
 
-  double ks[8];
+  // V's sequence mean (V_CENTERED): every block of the plane reduces the same partials in the
+  // same order, so all of them subtract the same bits.
+  float vmu[8];
+  if (VMODE == V_CENTERED) {
+    if (tid < HD) {
+      double sum = 0.0;
+      for (int64_t cc = 0; cc < C1; ++cc) sum += vpart[(bh * C1 + cc) * HD + tid];
+      const float m = (float)(sum / (double)N);
+      vmu_s[tid] = m;
+      if (c == 0) VMEAN[bh * HD + tid] = m;
+    }
+    __syncthreads();
 #pragma unroll
-  for (int i = 0; i < 8; ++i) ks[i] = 0.0;
+    for (int e = 0; e < 8; ++e) vmu[e] = vmu_s[8 * cg + e];
+  }
+
+  double ks[8], vs[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ks[i] = vs[i] = 0.0;
   float sv_max = 0.0f;
 
   for (int64_t n0 = r_begin; n0 < r_end; n0 += STEP) {
@@ -86,9 +116,9 @@ __global__ __launch_bounds__(PT) void kv_stats_kernel(
       const int64_t n = n0 + 8 * rg + i;
       const bool live = n < N;
       vw[i] = live ? *(const u32x4*)(vp + n * v_sr) : (u32x4){0u, 0u, 0u, 0u};
-      kw[i] = (live && smooth_k) ? *(const u32x4*)(kp + n * k_sr) : (u32x4){0u, 0u, 0u, 0u};
+      kw[i] = (live && k_sums) ? *(const u32x4*)(kp + n * k_sr) : (u32x4){0u, 0u, 0u, 0u};
     }
-    if (smooth_k) {
+    if (k_sums) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         float f[8];
@@ -97,6 +127,16 @@ __global__ __launch_bounds__(PT) void kv_stats_kernel(
         for (int e = 0; e < 8; ++e) ks[e] += (double)f[e];
       }
     }
+    if (VMODE == V_SUMS) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float f[8];
+        unpack8<T>(vw[i], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vs[e] += (double)f[e];
+      }
+      continue;
+    }
     // V: per-row scale and e4m3 bytes. col_lo/col_hi[e] collect tokens 0..3 / 4..7 of column e.
     uint32_t col_lo[8], col_hi[8];
 #pragma unroll
@@ -104,14 +144,19 @@ __global__ __launch_bounds__(PT) void kv_stats_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int64_t n = n0 + 8 * rg + i;
+      const bool live = n < N;
       float f[8];
       unpack8<T>(vw[i], f);
+      if (VMODE == V_CENTERED) {
+        // centred before the absmax; pad rows stay zero
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = live ? f[e] - vmu[e] : 0.0f;
+      }
       float vmax = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) vmax = fmaxf(vmax, fabsf(f[e]));
       vmax = max16(vmax);
       const float sv = fmaxf(__fdiv_rn(vmax, P_SCALE), SCALE_FLOOR);
-      const bool live = n < N;
       if (cg == 0 && n < N_pad) SV[bh * N_pad + n] = live ? sv : 0.0f;
       if (live) sv_max = fmaxf(sv_max, sv);
 #pragma unroll
@@ -148,8 +193,8 @@ __global__ __launch_bounds__(PT) void kv_stats_kernel(
   }
 
   // fp64 mean partials: reduce the 16 row groups in a fixed order.
-  if (smooth_k) {
-    double* red = (double*)tile;  // 16 x 128 doubles = 16 KB <= sizeof(tile)
+  double* red = (double*)tile;  // 16 x 128 doubles = 16 KB <= sizeof(tile)
+  if (k_sums) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) red[rg * HD + 8 * cg + e] = ks[e];
     __syncthreads();
@@ -159,6 +204,19 @@ __global__ __launch_bounds__(PT) void kv_stats_kernel(
       for (int r = 0; r < 16; ++r) s += red[r * HD + tid];
       part[(bh * C1 + c) * HD + tid] = s;
     }
+    __syncthreads();
+  }
+  if (VMODE == V_SUMS) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[rg * HD + 8 * cg + e] = vs[e];
+    __syncthreads();
+    if (tid < HD) {
+      double s = 0.0;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s += red[r * HD + tid];
+      vpart[(bh * C1 + c) * HD + tid] = s;
+    }
+    return;   // V is quantized by the V_CENTERED launch
   }
   // block max of sv over live rows
   float m = sv_max;
@@ -277,12 +335,29 @@ template <typename T>
 static hipError_t launch_prologue_t(const PrologueArgs& a, hipStream_t stream) {
   const int64_t BH = a.B * a.H;
   const PrologueGeom g = prologue_geom(BH, a.N_pad);
+  const size_t part_bytes = part_region_bytes(BH, g);
   double* part = (double*)a.workspace;
-  const size_t part_bytes = ((size_t)BH * g.C1 * HD * sizeof(double) + 255) / 256 * 256;
-  float* smax = (float*)((char*)a.workspace + part_bytes);
-  hipLaunchKernelGGL(kv_stats_kernel<T>, dim3((unsigned)g.C1, (unsigned)BH), dim3(PT), 0, stream,
-                     (const T*)a.k, (const T*)a.v, (u8*)a.v8t, a.sv, part, smax, a.H, a.N, a.N_pad,
-                     g.R1, g.C1, a.k_sb, a.k_sh, a.k_sr, a.v_sb, a.v_sh, a.v_sr, a.smooth_k);
+  double* vpart = (double*)((char*)a.workspace + part_bytes);
+  float* smax = (float*)((char*)a.workspace + 2 * part_bytes);
+  const dim3 grid1((unsigned)g.C1, (unsigned)BH);
+  if (a.smooth_v) {
+    // V's mean first (with K's partials), then V - mean quantized
+    hipLaunchKernelGGL((kv_stats_kernel<T, V_SUMS>), grid1, dim3(PT), 0, stream, (const T*)a.k,
+                       (const T*)a.v, (u8*)a.v8t, a.sv, part, vpart, a.vmean, smax, a.H, a.N,
+                       a.N_pad, g.R1, g.C1, a.k_sb, a.k_sh, a.k_sr, a.v_sb, a.v_sh, a.v_sr,
+                       a.smooth_k);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((kv_stats_kernel<T, V_CENTERED>), grid1, dim3(PT), 0, stream,
+                       (const T*)a.k, (const T*)a.v, (u8*)a.v8t, a.sv, part, vpart, a.vmean, smax,
+                       a.H, a.N, a.N_pad, g.R1, g.C1, a.k_sb, a.k_sh, a.k_sr, a.v_sb, a.v_sh,
+                       a.v_sr, a.smooth_k);
+  } else {
+    hipLaunchKernelGGL((kv_stats_kernel<T, V_QUANT>), grid1, dim3(PT), 0, stream, (const T*)a.k,
+                       (const T*)a.v, (u8*)a.v8t, a.sv, part, vpart, a.vmean, smax, a.H, a.N,
+                       a.N_pad, g.R1, g.C1, a.k_sb, a.k_sh, a.k_sr, a.v_sb, a.v_sh, a.v_sr,
+                       a.smooth_k);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (a.k_int8)

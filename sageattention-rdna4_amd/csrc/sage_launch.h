@@ -18,7 +18,7 @@ PrologueGeom prologue_geom(int64_t BH, int64_t N_pad);
 size_t prologue_workspace_bytes(int64_t BH, int64_t N_pad);
 
 struct PrologueArgs {
-  int dtype, k_int8, smooth_k, fold;
+  int dtype, k_int8, smooth_k, smooth_v, fold;
   const void* k;
   int64_t k_sb, k_sh, k_sr;
   const void* v;
@@ -29,6 +29,7 @@ struct PrologueArgs {
   void* v8t;
   float* sv;
   float* mean;
+  float* vmean;    // required with smooth_v: V's sequence mean (B*H, 128) fp32
   float* s;
   float* kconst;   // optional: the main loop's per-key constants (B*H, N_pad/64, 3, 64) fp32
   void* workspace;
@@ -50,6 +51,7 @@ struct AttnArgs {
   float sm_scale;
   float* lse;              // optional (B*H, N) fp32 row logsumexp
   const float* kmean;      // optional (B*H_kv, 128) fp32 smooth_k mean, for the logsumexp correction
+  const float* vmean;      // optional (B*H_kv, 128) fp32 smooth_v mean, added to the output
 };
 hipError_t launch_attn_fwd(const AttnArgs& a, hipStream_t stream);
 // the two-group ping-pong form of the same main loop (256 queries per block of 8 waves)

@@ -7,11 +7,14 @@ sk1_backend=None, sk1_int8=None, sk1_bf16=None, **kwargs)`, with `smooth_k` (def
 
 There is exactly one backend here, the gfx950 library. A call outside its envelope raises a clear
 error instead of silently falling back (the reference falls back to its PR #368 path): `attn_mask`
-raises `NotImplementedError` as in `core.py:1156-1161`; any other miss (smooth_v, head_dim != 128,
-H not a multiple of H_kv, causal with q_len != kv_len, other dtypes) raises `ValueError` naming
-the reason. `return_lse=True` returns `(out, lse)` with lse (B, H, N) fp32 as the reference's
-`core.py:1081-1095` defines it, and grouped K/V heads and a key length of their own are served
-as the upstream API serves them (`core.py:824-829`); the reference's SK1 path refuses all three.
+raises `NotImplementedError` as in `core.py:1156-1161`; any other miss (head_dim != 128, H not a
+multiple of H_kv, causal with q_len != kv_len, other dtypes) raises `ValueError` naming the
+reason. `return_lse=True` returns `(out, lse)` with lse (B, H, N) fp32 as the reference's
+`core.py:1081-1095` defines it; grouped K/V heads and a key length of their own are served as the
+upstream API serves them (`core.py:824-829`); `smooth_v=True` subtracts V's sequence mean before
+quantizing V and adds it back to the output (`core.py:395-421`; in the SK1 scheme the reference's
+`quant_triton.py:668-678` with the VMEAN epilogue of `kernels/hip/sk1_t6i.hip:290-297`). The
+reference's SK1 path refuses all four.
 """
 from .sk1_backend import try_sk1_t1
 
@@ -29,7 +32,8 @@ def sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=None, retur
     (N_kv == N when causal); fp16 or bf16, on a gfx950 device. Returns the output in q's layout
     and dtype; with `return_lse=True`, the pair `(out, lse)`, lse (B, H, N) fp32: the natural-log
     logsumexp of each row of Q.K^T * sm_scale.
-    kwargs: `smooth_k` (default True) subtracts the sequence mean of K before quantizing it.
+    kwargs: `smooth_k` (default True) subtracts the sequence mean of K before quantizing it;
+    `smooth_v` (default False) subtracts V's and adds it back to the output.
     `sk1_int8=False` selects fp8 Q.K for fp16 inputs; `sk1_backend` and `sk1_bf16` are accepted and
     ignored (there is one backend).
     """

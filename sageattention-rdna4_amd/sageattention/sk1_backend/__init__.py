@@ -39,7 +39,7 @@ ENVELOPE = dict(
     seq_len="N >= 1, N_kv >= 1; N == N_kv when causal",
     return_lse=(False, True),
     attn_mask=False,
-    smooth_v=False,
+    smooth_v=(False, True),
 )
 
 _LOGGED = set()
@@ -78,8 +78,6 @@ def _envelope_ok(q, k, v, tensor_layout, is_causal, sm_scale, return_lse, smooth
         return "layout"
     if attn_mask is not None:
         return "attn_mask"
-    if smooth_v:
-        return "smooth_v"
     if not (isinstance(q, torch.Tensor) and isinstance(k, torch.Tensor)
             and isinstance(v, torch.Tensor)):
         return "device"
@@ -152,7 +150,7 @@ def try_sk1_t1(q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=None, 
     try:
         out = sk1_forward(lib, q, k, v, tensor_layout=tensor_layout, is_causal=is_causal,
                           sm_scale=sm_scale, smooth_k=smooth_k, int8=int8,
-                          return_lse=bool(return_lse))
+                          return_lse=bool(return_lse), smooth_v=bool(smooth_v))
     except Exception as e:
         if strict:
             raise
@@ -162,10 +160,13 @@ def try_sk1_t1(q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=None, 
 
 
 def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=None,
-                smooth_k=True, int8=None, events=None, kernel=0, return_lse=False):
+                smooth_k=True, int8=None, events=None, kernel=0, return_lse=False,
+                smooth_v=False):
     """The served path without the envelope check: allocate, prologue (2 launches), main loop.
     q is (B, H, N, D) and k, v (B, H_kv, N_kv, D) in HND terms: query head h reads K/V head
-    h // (H // H_kv); N may differ from N_kv when not causal.
+    h // (H // H_kv); N may differ from N_kv when not causal. `smooth_v` subtracts V's sequence
+    mean before quantizing V and adds it back to the output (exact, since each row's weights sum
+    to 1; the reference's `quant_triton.py:668-678`).
     `kernel` picks the main-loop kernel (0: by size, 1: 128 queries per block, 2: 256).
     With `return_lse`, returns `(out, lse)`: lse (B, H, N) fp32, each row's natural-log
     logsumexp of its scores times sm_scale (with smooth_k, corrected by sm_scale * q . mean_k, as
@@ -198,6 +199,7 @@ def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=
     lse = torch.empty(B, H, N, device=dev, dtype=torch.float32) if return_lse else None
     kmean = (torch.empty(BH_kv, D, device=dev, dtype=torch.float32)
              if (return_lse and smooth_k) else None)
+    vmean = torch.empty(BH_kv, D, device=dev, dtype=torch.float32) if smooth_v else None
     if tensor_layout == "NHD":
         out = torch.empty(B, N, H, D, device=dev, dtype=q.dtype)
         oo = out.transpose(1, 2)
@@ -208,11 +210,13 @@ def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=
         if events is not None:
             events[0].record()
         lib.kv_prologue(kk, vv, k8, sk, v8t, sv, s, kmean, ws, k_int8=qk_int8,
-                        smooth_k=bool(smooth_k), fold=True, n_pad=n_pad, kconst=kconst)
+                        smooth_k=bool(smooth_k), fold=True, n_pad=n_pad, kconst=kconst,
+                        smooth_v=bool(smooth_v), vmean=vmean)
         if events is not None:
             events[1].record()
         lib.attn_fwd(qq, k8, kconst, v8t, s, oo, qk_int8=qk_int8, causal=bool(is_causal),
-                     sm_scale=sm, n_pad=n_pad, kernel=kernel, lse=lse, kmean=kmean, n_kv=N_kv)
+                     sm_scale=sm, n_pad=n_pad, kernel=kernel, lse=lse, kmean=kmean, n_kv=N_kv,
+                     vmean=vmean)
         if events is not None:
             events[2].record()
     return (out, lse) if return_lse else out

@@ -104,14 +104,15 @@ class SageLib:
         L.sage_kv_prologue_workspace_bytes.restype = ctypes.c_size_t
         L.sage_kv_prologue_workspace_bytes.argtypes = [i64, i64]
         L.sage_kv_prologue.restype = i32
-        L.sage_kv_prologue.argtypes = ([i32] * 4 + [vp, i64, i64, i64] * 2 + [i64] * 4
-                                       + [vp] * 8 + [ctypes.c_size_t, vp])
+        L.sage_kv_prologue.argtypes = ([i32] * 5 + [vp, i64, i64, i64] * 2 + [i64] * 4
+                                       + [vp] * 9 + [ctypes.c_size_t, vp])
         L.sage_attn_fwd.restype = i32
         L.sage_attn_fwd.argtypes = ([i32] * 3 + [vp, i64, i64, i64] + [vp] * 4
                                     + [vp, i64, i64, i64] + [i64] * 4 + [f32, vp])
         L.sage_attn_fwd_ex.restype = i32
         L.sage_attn_fwd_ex.argtypes = ([i32] * 3 + [vp, i64, i64, i64] + [vp] * 4
-                                       + [vp, i64, i64, i64] + [i64] * 6 + [f32, i32, vp, vp, vp])
+                                       + [vp, i64, i64, i64] + [i64] * 6
+                                       + [f32, i32, vp, vp, vp, vp])
         L.sage_quant_q.restype = i32
         L.sage_quant_q.argtypes = [i32, i32, vp, i64, i64, i64, i64, i64, i64, f32, vp, vp, vp, vp]
         L.sage_mfma_layout_probe.restype = i32
@@ -131,26 +132,29 @@ class SageLib:
 
     # ------------------------------------------------------------------ entry points
     def kv_prologue(self, k, v, k8, sk, v8t, sv, s, mean, workspace, *, k_int8, smooth_k, fold,
-                    n_pad, kconst=None):
+                    n_pad, kconst=None, smooth_v=False, vmean=None):
         """K/V prologue on logical (B, H, N, D) views `k`, `v` (see `sage_kv_prologue`).
-        `kconst` (optional) receives the main loop's per-key constants, (B*H, N_pad/64, 3, 64)."""
+        `kconst` (optional) receives the main loop's per-key constants, (B*H, N_pad/64, 3, 64);
+        with `smooth_v`, `vmean` ((B*H, 128) fp32) receives V's sequence mean."""
         B, H, N, _ = (int(x) for x in k.shape)
         rc = self.lib.sage_kv_prologue(
-            _dtype_code(k.dtype), int(bool(k_int8)), int(bool(smooth_k)), int(bool(fold)),
-            _ptr(k), k.stride(0), k.stride(1), k.stride(2),
+            _dtype_code(k.dtype), int(bool(k_int8)), int(bool(smooth_k)), int(bool(smooth_v)),
+            int(bool(fold)), _ptr(k), k.stride(0), k.stride(1), k.stride(2),
             _ptr(v), v.stride(0), v.stride(1), v.stride(2),
-            B, H, N, int(n_pad), _ptr(k8), _ptr(sk), _ptr(v8t), _ptr(sv), _ptr(mean), _ptr(s),
-            _ptr(kconst), _ptr(workspace), int(workspace.numel() * workspace.element_size()),
+            B, H, N, int(n_pad), _ptr(k8), _ptr(sk), _ptr(v8t), _ptr(sv), _ptr(mean),
+            _ptr(vmean), _ptr(s), _ptr(kconst), _ptr(workspace),
+            int(workspace.numel() * workspace.element_size()),
             ctypes.c_void_p(torch_stream(k.device)))
         self._check(rc, "sage_kv_prologue")
 
     def attn_fwd(self, q, k8, kconst, v8t, s, o, *, qk_int8, causal, sm_scale, n_pad, kernel=0,
-                 lse=None, kmean=None, n_kv=None):
+                 lse=None, kmean=None, n_kv=None, vmean=None):
         """Main loop on logical (B, H, N, D) views `q`, `o` (see `sage_attn_fwd_ex`; `kernel`:
         0 by size, 1 the 128-query kernel, 2 the 256-query ping-pong). The prologue outputs
         `k8` (B*H_kv, n_pad, D) etc. give H_kv; `n_kv` is the key count (default N, and `n_pad`
         is then ceil(n_kv/64)*64). `lse` (optional, (B, H, N) fp32) receives each row's
-        logsumexp; `kmean` ((B*H_kv, 128) fp32) adds its smooth_k correction."""
+        logsumexp; `kmean` ((B*H_kv, 128) fp32) adds its smooth_k correction; `vmean`
+        ((B*H_kv, 128) fp32, optional) is added to every output row (smooth_v)."""
         B, H, N, _ = (int(x) for x in q.shape)
         bh_kv = int(k8.shape[0])
         if bh_kv % B:
@@ -162,7 +166,7 @@ class SageLib:
             _ptr(k8), _ptr(kconst), _ptr(v8t), _ptr(s),
             _ptr(o), o.stride(0), o.stride(1), o.stride(2),
             B, H, N, bh_kv // B, n_kv, int(n_pad), ctypes.c_float(float(sm_scale)), int(kernel),
-            _ptr(lse), _ptr(kmean), ctypes.c_void_p(torch_stream(q.device)))
+            _ptr(lse), _ptr(kmean), _ptr(vmean), ctypes.c_void_p(torch_stream(q.device)))
         self._check(rc, "sage_attn_fwd")
 
     def quant_q(self, q, sm_scale, *, qk_int8):

@@ -27,7 +27,8 @@ import oracle  # noqa: E402
 from sage_testutil import make_qkv  # noqa: E402
 
 CASES = {
-    # name: (dtype, B, H, N, causal, smooth_k, layout, std, k_offset, outliers, seed[, H_kv, N_kv])
+    # name: (dtype, B, H, N, causal, smooth_k, layout, std, k_offset, outliers, seed
+    #        [, H_kv, N_kv[, smooth_v, v_offset]])
     "fp16_n77_causal": (torch.float16, 1, 1, 77, True, True, "HND", 1.0, 2.0, 0.03, 11),
     "fp16_n1_noncausal": (torch.float16, 1, 2, 1, False, True, "HND", 1.0, 2.0, 0.0, 12),
     "fp16_n70_nhd_nosmooth": (torch.float16, 2, 1, 70, False, False, "NHD", 1.0, 0.0, 0.0, 13),
@@ -37,6 +38,11 @@ CASES = {
                                  2, 130),
     "bf16_mqa_nhd_n100_kv37": (torch.bfloat16, 2, 3, 100, False, True, "NHD", 1.0, 1.0, 0.0, 16,
                                1, 37),
+    # smooth_v on V with per-channel offsets
+    "fp16_smoothv_n100_causal": (torch.float16, 1, 2, 100, True, True, "HND", 1.0, 2.0, 0.0, 17,
+                                 2, 100, True, 4.0),
+    "bf16_smoothv_gqa_n80_kv150": (torch.bfloat16, 1, 4, 80, False, False, "HND", 1.0, 0.0, 0.0,
+                                   18, 2, 150, True, 3.0),
 }
 
 
@@ -63,15 +69,17 @@ def corner_rows(q, k, v, layout):
 
 def make(name):
     dtype, B, H, N, causal, smooth_k, layout, std, off, outl, seed = CASES[name][:11]
-    H_kv, N_kv = CASES[name][11:] or (H, N)
+    H_kv, N_kv = CASES[name][11:13] or (H, N)
+    smooth_v, v_off = CASES[name][13:15] or (False, 0.0)
     q, k, v = make_qkv(B, H, N, seed=seed, dtype=dtype, layout=layout, std=std, k_offset_std=off,
-                       outlier_frac=outl, h_kv=H_kv, n_kv=N_kv)
+                       outlier_frac=outl, h_kv=H_kv, n_kv=N_kv, v_offset_std=v_off)
     q, k, v = corner_rows(q, k, v, layout)
-    r = oracle.emulate_sageattn(q, k, v, tensor_layout=layout, is_causal=causal, smooth_k=smooth_k)
+    r = oracle.emulate_sageattn(q, k, v, tensor_layout=layout, is_causal=causal, smooth_k=smooth_k,
+                                smooth_v=smooth_v)
     arr = dict(
-        # B, H, N, causal, smooth_k, NHD, bf16, H_kv, N_kv
+        # B, H, N, causal, smooth_k, NHD, bf16, H_kv, N_kv, smooth_v
         meta=np.array([B, H, N, int(causal), int(smooth_k), int(layout == "NHD"),
-                       int(dtype == torch.bfloat16), H_kv, N_kv], dtype=np.int64),
+                       int(dtype == torch.bfloat16), H_kv, N_kv, int(smooth_v)], dtype=np.int64),
         sm_scale=np.array([r["sm_scale"]], dtype=np.float32),
         q=bits(q), k=bits(k), v=bits(v),
         k8=bits(r["k8"]) if r["k8"].dtype != torch.int8 else r["k8"].numpy(),
@@ -81,6 +89,8 @@ def make(name):
     )
     if r["mean"] is not None:
         arr["mean"] = r["mean"].numpy()
+    if r["vmean"] is not None:
+        arr["vmean"] = r["vmean"].numpy()
     return arr
 
 

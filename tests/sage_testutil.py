@@ -15,14 +15,16 @@ def have_gfx950():
 
 
 def make_qkv(b, h, n, *, seed=0, dtype=torch.float16, layout="HND", std=1.0, k_offset_std=0.0,
-             outlier_frac=0.0, outlier_scale=50.0, d=HEAD_DIM, h_kv=None, n_kv=None):
+             outlier_frac=0.0, outlier_scale=50.0, d=HEAD_DIM, h_kv=None, n_kv=None,
+             v_offset_std=0.0):
     """Seeded CPU tensors, cast to `dtype` (the GPU and the oracle then see identical bytes).
 
     Q, K, V ~ N(0, std). K gets a per-(b,h) channel offset mu ~ N(0, k_offset_std) broadcast over
     tokens, and `round(outlier_frac * n_kv)` K rows per plane (seeded choice) are scaled by
     `outlier_scale` -- the synthetic inputs of the benchmark configurations. K and V have `h_kv`
     heads and `n_kv` rows (default h and n; with the defaults the draws are the same as before
-    these parameters existed).
+    these parameters existed). V gets a per-(b,h) channel offset ~ N(0, v_offset_std), drawn
+    last.
     Returns (q, k, v) in `layout` ("HND" (B,H,N,D) or "NHD" (B,N,H,D)), contiguous.
     """
     hk = h if h_kv is None else h_kv
@@ -39,6 +41,8 @@ def make_qkv(b, h, n, *, seed=0, dtype=torch.float16, layout="HND", std=1.0, k_o
             for hi in range(hk):
                 idx = torch.randperm(nk, generator=g)[:n_out]
                 k[bi, hi, idx] *= outlier_scale
+    if v_offset_std:
+        v = v + torch.randn(b, hk, 1, d, generator=g) * v_offset_std
     out = [t.to(dtype) for t in (q, k, v)]
     if layout == "NHD":
         out = [t.transpose(1, 2).contiguous() for t in out]

@@ -26,13 +26,13 @@ def _load(path):
 
 
 def _inputs(g):
-    B, H, N, causal, smooth_k, nhd, bf16, H_kv, N_kv = (int(x) for x in g["meta"])
+    B, H, N, causal, smooth_k, nhd, bf16, H_kv, N_kv, smooth_v = (int(x) for x in g["meta"])
     dtype = torch.bfloat16 if bf16 else torch.float16
     shape = (B, N, H, 128) if nhd else (B, H, N, 128)
     kv_shape = (B, N_kv, H_kv, 128) if nhd else (B, H_kv, N_kv, 128)
     q = torch.from_numpy(g["q"].astype(np.int16)).view(dtype).reshape(shape)
     k, v = (torch.from_numpy(g[n].astype(np.int16)).view(dtype).reshape(kv_shape) for n in "kv")
-    return q, k, v, dict(causal=bool(causal), smooth_k=bool(smooth_k),
+    return q, k, v, dict(causal=bool(causal), smooth_k=bool(smooth_k), smooth_v=bool(smooth_v),
                          layout="NHD" if nhd else "HND", dtype=dtype)
 
 
@@ -54,11 +54,13 @@ def test_oracle_reproduces_fixture(path):
     g = _load(path)
     q, k, v, m = _inputs(g)
     r = oracle.emulate_sageattn(q, k, v, tensor_layout=m["layout"], is_causal=m["causal"],
-                                smooth_k=m["smooth_k"])
+                                smooth_k=m["smooth_k"], smooth_v=m["smooth_v"])
     for name in ("k8", "sk", "v8t", "sv", "s", "svp", "q8", "sq", "c_q", "o", "lse"):
         assert np.array_equal(_bits(r[name]), g[name]), name
     if m["smooth_k"]:
         assert np.array_equal(r["mean"].numpy(), g["mean"])
+    if m["smooth_v"]:
+        assert np.array_equal(r["vmean"].numpy(), g["vmean"])
     assert np.float32(r["sm_scale"]) == g["sm_scale"][0]
 
 
@@ -82,18 +84,21 @@ def test_gpu_matches_fixture(path):
     v8t = torch.empty(BH, D, n_pad, device=dev, dtype=torch.float8_e4m3fn)
     sk, sv = (torch.empty(BH, n_pad, device=dev) for _ in range(2))
     s, mean = torch.empty(BH, device=dev), torch.empty(BH, D, device=dev)
+    vmean = torch.empty(BH, D, device=dev)
     ws = torch.empty(lib.workspace_bytes(BH, N), device=dev, dtype=torch.uint8)
     lib.kv_prologue(kk, vv, k8, sk, v8t, sv, s, mean, ws, k_int8=int8, smooth_k=m["smooth_k"],
-                    fold=True, n_pad=n_pad)
+                    fold=True, n_pad=n_pad, smooth_v=m["smooth_v"], vmean=vmean)
     q8, sq, cq = lib.quant_q(qq, float(g["sm_scale"][0]), qk_int8=int8)
     out, lse = sageattn(qd, kd, vd, tensor_layout=m["layout"], is_causal=m["causal"],
-                        smooth_k=m["smooth_k"], return_lse=True)
+                        smooth_k=m["smooth_k"], smooth_v=m["smooth_v"], return_lse=True)
     torch.cuda.synchronize()
     got = dict(k8=k8, v8t=v8t, sk=sk, svp=sv, s=s, q8=q8, sq=sq, c_q=cq)
     for name, t in got.items():
         assert np.array_equal(_bits(t.cpu()), g[name]), name
     if m["smooth_k"]:
         assert np.array_equal(mean.cpu().numpy(), g["mean"])
+    if m["smooth_v"]:
+        assert np.array_equal(vmean.cpu().numpy(), g["vmean"])
     ref = torch.from_numpy(g["o"].astype(np.int16)).view(m["dtype"]).reshape(out.shape)
     c, r1 = cosine(out.cpu(), ref), rel_l1(out.cpu(), ref)
     print("cos %.6f rel_l1 %.3e" % (c, r1), flush=True)

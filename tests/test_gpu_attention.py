@@ -391,3 +391,61 @@ def test_gqa_refusals_raise():
         _sageattn()(q, k2, k2, is_causal=True)
     with pytest.raises(ValueError, match="seq_len"):
         _sageattn()(q, k2, k2[:, :, :64])
+
+
+# ---------------------------------------------------------------------------------------------
+# smooth_v: V's sequence mean subtracted before quantizing V and added back in the epilogue
+# (the reference's `quant_triton.py:668-678` with the VMEAN epilogue of `sk1_t6i.hip:290-297`;
+# its SK1 envelope refuses it). Bars as above against the emulation; on V with per-channel
+# offsets it must beat the plain path against exact attention (the reference's F005 finding).
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("layout", ["HND", "NHD"])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N", [1, 65, 300, 1337])
+def test_smooth_v_matches_emulation(N, dtype, causal, layout):
+    q, k, v = make_qkv(1, 3, N, seed=N + 11, dtype=dtype, layout=layout, k_offset_std=2.0,
+                       v_offset_std=4.0)
+    print("N", N, dtype, causal, layout, flush=True)
+    r = oracle.emulate_sageattn(q, k, v, tensor_layout=layout, is_causal=causal, smooth_v=True)
+    out = _sageattn()(q.cuda(), k.cuda(), v.cuda(), tensor_layout=layout, is_causal=causal,
+                      smooth_v=True).cpu()
+    cs, rl = cosine(out, r["o"]), rel_l1(out, r["o"])
+    print("cos %.6f rel_l1 %.2e" % (cs, rl))
+    assert cs >= COS_MIN and rl <= REL_L1_MAX, (cs, rl)
+    if N > 1:
+        ex = oracle.exact_attention(q, k, v, is_causal=causal, tensor_layout=layout)
+        plain = _sageattn()(q.cuda(), k.cuda(), v.cuda(), tensor_layout=layout,
+                            is_causal=causal).cpu()
+        e_sv, e_plain = rel_rms(out, ex), rel_rms(plain, ex)
+        print("rel_rms vs exact: smooth_v %.3e plain %.3e" % (e_sv, e_plain))
+        assert e_sv < e_plain
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_smooth_v_identical_rows_give_the_row_exactly(dtype):
+    # every token's V equal to one vector c: the centred V is 0, so O = T(fma(0, inv, c)) = c
+    q, k, v = make_qkv(2, 3, 200, seed=4, dtype=dtype, k_offset_std=1.0)
+    v[:] = v[:, :, :1]
+    for causal in (False, True):
+        out = _sageattn()(q.cuda(), k.cuda(), v.cuda(), is_causal=causal, smooth_v=True).cpu()
+        assert torch.equal(out, v.expand_as(out))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_smooth_v_both_kernels_and_gqa_bitwise(causal):
+    from sageattention.sk1_backend import sk1_forward
+    from sageattention.sk1_backend.sk1_loader import SageLib
+    lib = SageLib.get()
+    q, k, v = make_qkv(1, 6, 777, seed=13, dtype=torch.bfloat16, h_kv=2, k_offset_std=2.0,
+                       v_offset_std=3.0)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    o1, l1 = sk1_forward(lib, qd, kd, vd, is_causal=causal, kernel=1, smooth_v=True,
+                         return_lse=True)
+    o2 = sk1_forward(lib, qd, kd, vd, is_causal=causal, kernel=2, smooth_v=True)
+    o_rep = sk1_forward(lib, qd, kd.repeat_interleave(3, 1), vd.repeat_interleave(3, 1),
+                        is_causal=causal, kernel=1, smooth_v=True)
+    _, l_plain = sk1_forward(lib, qd, kd, vd, is_causal=causal, kernel=1, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(o1, o_rep)
+    assert torch.equal(l1, l_plain)          # the scores, and so the logsumexp, do not involve V

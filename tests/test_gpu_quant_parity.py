@@ -19,7 +19,8 @@ def _lib():
     return SageLib.get()
 
 
-def _run_prologue(k, v, *, k_int8, smooth_k, fold, layout="HND", with_kconst=False):
+def _run_prologue(k, v, *, k_int8, smooth_k, fold, layout="HND", with_kconst=False,
+                  smooth_v=False):
     lib = _lib()
     kk, vv = (oracle.to_hnd(t, layout) for t in (k, v))
     B, H, N, D = kk.shape
@@ -33,28 +34,31 @@ def _run_prologue(k, v, *, k_int8, smooth_k, fold, layout="HND", with_kconst=Fal
     sv = torch.full((BH, n_pad), float("nan"), device=dev)
     s = torch.full((BH,), float("nan"), device=dev)
     mean = torch.full((BH, D), float("nan"), device=dev)
+    vmean = torch.full((BH, D), float("nan"), device=dev)
     ws = torch.full((lib.workspace_bytes(BH, N),), 0xFF, device=dev, dtype=torch.uint8)
     kc = (torch.full((BH, n_pad // 64, 3, 64), float("nan"), device=dev) if with_kconst
           else None)
     lib.kv_prologue(kk, vv, k8, sk, v8t, sv, s, mean, ws, k_int8=k_int8, smooth_k=smooth_k,
-                    fold=fold, n_pad=n_pad, kconst=kc)
+                    fold=fold, n_pad=n_pad, kconst=kc, smooth_v=smooth_v, vmean=vmean)
     torch.cuda.synchronize()
-    out = dict(k8=k8.cpu(), sk=sk.cpu(), v8t=v8t.cpu(), sv=sv.cpu(), s=s.cpu(), mean=mean.cpu())
+    out = dict(k8=k8.cpu(), sk=sk.cpu(), v8t=v8t.cpu(), sv=sv.cpu(), s=s.cpu(), mean=mean.cpu(),
+               vmean=vmean.cpu())
     if with_kconst:
         out["kconst"] = kc.cpu()
     return out
 
 
-def _oracle_prologue(k, v, *, k_int8, smooth_k, layout="HND"):
+def _oracle_prologue(k, v, *, k_int8, smooth_k, layout="HND", smooth_v=False):
     kk, vv = (oracle.to_hnd(t, layout) for t in (k, v))
     B, H, N, D = kk.shape
     kr, vr = kk.reshape(B * H, N, D), vv.reshape(B * H, N, D)
     n_pad = oracle.n_pad_for(N)
     mean = oracle.kseq_mean(kr) if smooth_k else None
+    vmean = oracle.kseq_mean(vr) if smooth_v else None
     k8, sk = oracle.quant_k(kr, n_pad, mean=mean, int8=k_int8)
-    v8t, sv = oracle.quant_v(vr, n_pad)
+    v8t, sv = oracle.quant_v(vr, n_pad, mean=vmean)
     s, svp = oracle.fold_v_scale(sv)
-    return dict(mean=mean, k8=k8, sk=sk, v8t=v8t, sv=sv, s=s, svp=svp)
+    return dict(mean=mean, vmean=vmean, k8=k8, sk=sk, v8t=v8t, sv=sv, s=s, svp=svp)
 
 
 CASES = [
@@ -91,6 +95,32 @@ def test_prologue_bit_exact(case, smooth_k):
     folded = _run_prologue(k.cuda(), v.cuda(), k_int8=k_int8, smooth_k=smooth_k, fold=True)
     assert bytes_equal(folded["sv"], ref["svp"]), mismatch_report(folded["sv"], ref["svp"], "svp")
     assert bytes_equal(folded["k8"], ref["k8"])
+
+
+@pytest.mark.parametrize("smooth_k", [True, False])
+@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[3], CASES[4], CASES[6], CASES[8],
+                                  CASES[10], CASES[11]], ids=lambda c: "%s-%s-N%d" % (
+    str(c[0]).split(".")[-1], "i8" if c[1] else "f8", c[2]))
+def test_prologue_smooth_v_bit_exact(case, smooth_k):
+    # smooth_v: V's fp64 sequence mean, V centred before its per-token scale (a second stats
+    # launch); K's outputs must not move; S > 1 (a V row far above 448) exercises the fold.
+    dtype, k_int8, N, H, off, outl, std = case
+    q, k, v = make_qkv(1, H, N, seed=N + 2 * H, dtype=dtype, std=std, k_offset_std=off,
+                       outlier_frac=outl, v_offset_std=3.0)
+    if N > 5:
+        v[0, 0, 5] = 3000.0
+    print("case", case, "smooth_k", smooth_k, flush=True)
+    ref = _oracle_prologue(k, v, k_int8=k_int8, smooth_k=smooth_k, smooth_v=True)
+    got = _run_prologue(k.cuda(), v.cuda(), k_int8=k_int8, smooth_k=smooth_k, fold=True,
+                        smooth_v=True)
+    assert bytes_equal(got["vmean"], ref["vmean"]), mismatch_report(got["vmean"], ref["vmean"],
+                                                                    "vmean")
+    if smooth_k:
+        assert bytes_equal(got["mean"], ref["mean"]), mismatch_report(got["mean"], ref["mean"], "mean")
+    for name, rname in (("k8", "k8"), ("sk", "sk"), ("v8t", "v8t"), ("sv", "svp"), ("s", "s")):
+        assert bytes_equal(got[name], ref[rname]), mismatch_report(got[name], ref[rname], name)
+    plain = _run_prologue(k.cuda(), v.cuda(), k_int8=k_int8, smooth_k=smooth_k, fold=True)
+    assert bytes_equal(plain["k8"], got["k8"]) and bytes_equal(plain["sk"], got["sk"])
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

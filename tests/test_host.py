@@ -54,11 +54,11 @@ def test_library_host_calls_without_a_gpu():
     rc = L.lib.sage_attn_fwd(0, 1, 1, None, 8, 8, 8, None, None, None, None, None, 8, 8, 8,
                              1, 1, 0, 64, ctypes.c_float(0.1), None)
     assert rc == 1 and b"n_lt_1" in L.lib.sage_last_error()
-    rc = L.lib.sage_kv_prologue(1, 1, 1, 1, None, 8, 8, 8, None, 8, 8, 8, 1, 1, 10, 64,
-                                *([None] * 8), 0, None)
+    rc = L.lib.sage_kv_prologue(1, 1, 1, 0, 1, None, 8, 8, 8, None, 8, 8, 8, 1, 1, 10, 64,
+                                *([None] * 9), 0, None)
     assert rc == 1 and b"bf16_int8" in L.lib.sage_last_error()
-    rc = L.lib.sage_kv_prologue(0, 1, 1, 1, ctypes.c_void_p(16), 8, 8, 4, ctypes.c_void_p(16),
-                                8, 8, 8, 1, 1, 10, 64, *([None] * 8), 0, None)
+    rc = L.lib.sage_kv_prologue(0, 1, 1, 0, 1, ctypes.c_void_p(16), 8, 8, 4, ctypes.c_void_p(16),
+                                8, 8, 8, 1, 1, 10, 64, *([None] * 9), 0, None)
     assert rc == 1 and b"stride_align" in L.lib.sage_last_error()
     rc = L.lib.sage_attn_fwd(0, 1, 0, ctypes.c_void_p(16), 8, 8, 8, None, None, None, None,
                              ctypes.c_void_p(16), 8, 8, 8, 1, 1, 100, 96, ctypes.c_float(0.1), None)
@@ -67,7 +67,7 @@ def test_library_host_calls_without_a_gpu():
     def ex(causal=0, H=1, N=100, H_kv=1, N_kv=100, N_kv_pad=128, kernel=0, lse=None):
         return L.lib.sage_attn_fwd_ex(0, 1, causal, p16, 12800, 12800, 128, p16, p16, p16, p16,
                                       p16, 12800, 12800, 128, 1, H, N, H_kv, N_kv, N_kv_pad,
-                                      ctypes.c_float(0.1), kernel, lse, None, None)
+                                      ctypes.c_float(0.1), kernel, lse, None, None, None)
     assert ex(kernel=7) == 1 and b"kernel" in L.lib.sage_last_error()
     assert ex(lse=ctypes.c_void_p(18)) == 1
     assert b"lse must be 4-byte aligned" in L.lib.sage_last_error()
@@ -77,6 +77,11 @@ def test_library_host_calls_without_a_gpu():
     assert ex(causal=1, N_kv=99) == 1 and b"seq_len" in L.lib.sage_last_error()
     assert ex(N_kv=200, N_kv_pad=192) == 1 and b"n_pad" in L.lib.sage_last_error()
     assert ex(N_kv=0, N_kv_pad=64) == 1 and b"n_lt_1" in L.lib.sage_last_error()
+    # smooth_v needs somewhere to put V's mean
+    rc = L.lib.sage_kv_prologue(0, 1, 1, 1, 1, p16, 12800, 12800, 128, p16, 12800, 12800, 128,
+                                1, 1, 100, 128, p16, p16, p16, p16, None, None, p16, None, p16,
+                                1 << 20, None)
+    assert rc == 1 and b"vmean" in L.lib.sage_last_error()
 
 
 def test_strided_view_reason_rule():
@@ -108,7 +113,8 @@ def test_envelope_reasons_on_cpu_tensors():
     # return_lse is served here (the reference's SK1 path refuses it): CPU tensors then fail
     # on the device check, not on return_lse
     assert _envelope_ok(q, q, q, **dict(args, return_lse=True)) == "device"
-    assert _envelope_ok(q, q, q, **dict(args, smooth_v=True)) == "smooth_v"
+    # smooth_v is served too (the reference's SK1 envelope refuses it)
+    assert _envelope_ok(q, q, q, **dict(args, smooth_v=True)) == "device"
     assert _envelope_ok(q, q, q, **dict(args, attn_mask=torch.ones(1))) == "attn_mask"
     assert _envelope_ok(q, q, q, **args) == "device"
 

@@ -489,3 +489,81 @@ def test_gqa_and_kv_length_close_to_exact_attention():
         ex = oracle.exact_attention(q, k, v)
         rel = ((o - ex).pow(2).mean().sqrt() / ex.pow(2).mean().sqrt()).item()
         assert rel < 0.08, (dtype, rel)
+
+
+# ----------------------------------------------------------------------------- smooth_v
+def test_smooth_v_mean_is_fsum_of_v_and_centering_precedes_the_scale():
+    # V's mean is the same fp64 sequence mean as K's, and V is centred (fp32) before its absmax:
+    # SV = max(RN(max_d |RN(v - mu)| / 448), 1e-12) on live rows, V8T the e4m3 of RN(RN(v - mu)/SV).
+    q, k, v = make_qkv(1, 2, 77, seed=41)
+    v = (v.float() + 3.0).half()                             # a per-channel offset
+    r = oracle.emulate_sageattn(q, k, v, smooth_v=True, smooth_k=False)
+    vr = v.reshape(2, 77, 128)
+    for bh in range(2):
+        for d in (0, 63, 127):
+            col = [float(x) for x in vr[bh, :, d].float().tolist()]
+            assert f32_bits(r["vmean"][bh, d].item()) == f32_bits(float(np.float32(math.fsum(col) / 77)))
+        for n in (0, 40, 76):
+            c = [np.float32(np.float32(x) - np.float32(r["vmean"][bh, d].item()))
+                 for d, x in enumerate(vr[bh, n].float().tolist())]
+            sv = max(np.float32(max(abs(x) for x in c) / np.float32(448)), np.float32(1e-12))
+            assert f32_bits(r["sv"][bh, n].item()) == f32_bits(float(sv))
+            want = [e4m3_code(min(Fraction(float(np.float32(x / sv))), Fraction(448))) for x in c]
+            assert r["v8t"][bh, :, n].contiguous().view(torch.uint8).tolist() == want
+        assert r["v8t"][bh, :, 77:].float().abs().max().item() == 0.0     # pad rows stay zero
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_smooth_v_identical_rows_give_the_row_exactly(dtype):
+    # Every token's V equal to one vector c: the centred V is exactly 0, so the output is
+    # T(RN(0 + mean)) = c bit for bit, for every query, whatever the scores are.
+    q, k, v = make_qkv(2, 2, 90, seed=9, dtype=dtype)
+    v[:] = v[:, :, :1]
+    for causal in (False, True):
+        o = oracle.emulate_sageattn(q, k, v, is_causal=causal, smooth_v=True)["o"]
+        assert torch.equal(o, v.expand_as(o))
+        o_plain = oracle.emulate_sageattn(q, k, v, is_causal=causal)["o"]
+        assert not torch.equal(o_plain, v.expand_as(o))        # quantized V does not round-trip
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_smooth_v_vs_brute_force(causal):
+    N = 130
+    q, k, v = make_qkv(1, 1, N, seed=17, k_offset_std=1.0)
+    v = (v.float() * 0.5 + 2.5).half()
+    r = oracle.emulate_sageattn(q, k, v, is_causal=causal, smooth_v=True)
+    k8 = r["k8"][0].numpy().astype(np.int32)
+    v8t = r["v8t"][0].float().numpy()
+    q8 = r["q8"][0].numpy().astype(np.int32)
+    out = r["o"][0, 0].float().numpy()
+    vm = r["vmean"][0].numpy()
+    for row in (0, 1, 64, N - 1):
+        base = _brute_force_row(q8[row], r["c_q"][0, row].item(), k8, r["sk"][0].numpy(), v8t,
+                                r["svp"][0].numpy(), r["s"][0].item(), row, N, causal, True)
+        # the epilogue's fma(acc, inv, vm), from the brute-force acc*inv (one rounding apart)
+        want = (base.astype(np.float64) + vm.astype(np.float64)).astype(np.float32)
+        assert np.allclose(out[row], want.astype(np.float16).astype(np.float32), rtol=2e-3,
+                           atol=2e-3), row
+
+
+def test_smooth_v_wins_on_offset_v_and_the_add_back_is_needed(monkeypatch):
+    # The reference's finding (docs/FINDINGS.md F005): with a per-channel V offset of 6, centring
+    # before the per-token scale is far more accurate. A dropped add-back fails the same check.
+    import oracle.sage_scheme as mod
+    q, k, v = make_qkv(1, 2, 400, seed=5)
+    off = torch.randn(1, 2, 1, 128, generator=torch.Generator().manual_seed(3)) * 6.0
+    v = (v.float() * 0.3 + off).half()
+    ex = oracle.exact_attention(q, k, v)
+    err_plain = (oracle.emulate_sageattn(q, k, v)["o"].double() - ex).abs().max().item()
+    err_sv = (oracle.emulate_sageattn(q, k, v, smooth_v=True)["o"].double() - ex).abs().max().item()
+    assert err_sv * 10 < err_plain, (err_sv, err_plain)
+
+    import inspect
+    src = inspect.getsource(mod.attention_tiles)
+    old = "+ vmean.double()[:, None, :]"
+    assert src.count(old) == 1
+    ns = dict(vars(mod))
+    exec(compile(src.replace(old, ""), "<planted>", "exec"), ns)
+    monkeypatch.setattr(mod, "attention_tiles", ns["attention_tiles"])
+    err_planted = (mod.emulate_sageattn(q, k, v, smooth_v=True)["o"].double() - ex).abs().max().item()
+    assert err_planted > 1.0
