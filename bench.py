@@ -30,7 +30,7 @@ PEAK_TOPS = 5000.0          # MI355X dense int8 (5.0 POPS) and fp8 (5.0 PFLOP/s)
 HBM_PEAK_GBPS = 8000.0
 
 WORKLOADS = {
-    # name: (dtype, B, H, N, causal, layout, k_offset_std, outlier_frac, std)
+    # name: (dtype, B, H, N, causal, layout, k_offset_std, outlier_frac, std[, head_dim])
     "c3c": ("fp16", 1, 48, 47520, True, "HND", 2.0, 0.0, 1.0),     # headline (configs[2], causal)
     "c3n": ("fp16", 1, 48, 47520, False, "HND", 2.0, 0.0, 1.0),
     "c2c": ("fp16", 1, 48, 8771, True, "HND", 2.0, 0.001, 1.0),
@@ -40,7 +40,16 @@ WORKLOADS = {
     "c5_288": ("fp16", 1, 48, 288, False, "HND", 0.0, 0.0, 1.0),
     "c5_4096": ("fp16", 1, 48, 4096, False, "HND", 0.0, 0.0, 1.0),
     "c5_b8": ("fp16", 8, 24, 4096, False, "NHD", 0.0, 0.0, 1.0),
+    # head_dim 64: the reference's F165 shapes (SDXL 1024^2 level 1, CogVideoX-2B) and the
+    # headline length
+    "d64_sdxl": ("fp16", 1, 10, 4096, False, "HND", 2.0, 0.0, 1.0, 64),
+    "d64_cogvx": ("fp16", 1, 30, 17550, False, "HND", 2.0, 0.0, 1.0, 64),
+    "d64_c3c": ("fp16", 1, 48, 47520, True, "HND", 2.0, 0.0, 1.0, 64),
 }
+
+
+def head_dim(wl):
+    return wl[9] if len(wl) > 9 else 128
 
 
 def log(*a):
@@ -49,16 +58,17 @@ def log(*a):
 
 def make_inputs(wl, seed=0):
     import torch
-    dt, B, H, N, causal, layout, off, outl, std = wl
+    dt, B, H, N, causal, layout, off, outl, std = wl[:9]
+    D = head_dim(wl)
     dtype = torch.float16 if dt == "fp16" else torch.bfloat16
     g = torch.Generator().manual_seed(seed)
     out = []
     for i in range(3):
-        x = torch.randn(B, H, N, 128, generator=g, dtype=torch.float32)
+        x = torch.randn(B, H, N, D, generator=g, dtype=torch.float32)
         if std != 1.0:
             x.mul_(std)
         if i == 1 and off:
-            x.add_(torch.randn(B, H, 1, 128, generator=g) * off)
+            x.add_(torch.randn(B, H, 1, D, generator=g) * off)
         if i == 1 and outl:
             n_out = int(round(outl * N))
             for b in range(B):
@@ -72,16 +82,16 @@ def make_inputs(wl, seed=0):
     return out
 
 
-def ops_of(B, H, N, causal):
-    return 4.0 * B * H * N * N * 128 * (0.5 if causal else 1.0)
+def ops_of(B, H, N, causal, D=128):
+    return 4.0 * B * H * N * N * D * (0.5 if causal else 1.0)
 
 
-def prologue_bytes(B, H, N, smooth_k=True):
+def prologue_bytes(B, H, N, smooth_k=True, D=128):
     """Algorithmic HBM bytes of the prologue pair: K read twice (mean + quant) when smooth_k, V read
     once, K8 and V8T written, SK and SV written, SV read and rewritten by the fold."""
     n_pad = (N + 63) // 64 * 64
-    el = B * H * N * 128 * 2
-    q8 = B * H * n_pad * 128
+    el = B * H * N * D * 2
+    q8 = B * H * n_pad * D
     return (2 if smooth_k else 1) * el + el + 2 * q8 + 4 * B * H * n_pad * 4
 
 
@@ -112,7 +122,8 @@ def cpu_baseline(wl, q, k, v, budget_s=20.0):
     dt, B, H, N, causal, layout, *_ = wl
     qh, kh, vh = (oracle.to_hnd(t, layout)[0:1, 0:1].contiguous() for t in (q, k, v))
     n_pad = oracle.n_pad_for(N)
-    sm = 128 ** -0.5
+    D = head_dim(wl)
+    sm = D ** -0.5
     int8 = dt == "fp16"
 
     def run(rows):
@@ -134,7 +145,7 @@ def cpu_baseline(wl, q, k, v, budget_s=20.0):
         else:
             F.scaled_dot_product_attention(qs, kr.float(), vr.float())
         t_sdpa = time.perf_counter() - t0
-        ops = sum(4.0 * 128 * ((r + 1) if causal else N) for r in range(r0, N))
+        ops = sum(4.0 * D * ((r + 1) if causal else N) for r in range(r0, N))
         return ops, t_emu, t_sdpa
 
     # Two short runs fix the sample's fixed cost (the plane's prologue) and its cost per query row;
@@ -195,14 +206,16 @@ def main():
 
     wl = WORKLOADS[args.workload]
     dt, B, H, N, causal, layout, *_ = wl
+    D = head_dim(wl)
     q, k, v = make_inputs(wl)
     dev = torch.device("cuda:0")
     qd, kd, vd = (t.to(dev) for t in (q, k, v))
     lib = SageLib.get()
     call = lambda ev=None: sk1_forward(lib, qd, kd, vd, tensor_layout=layout, is_causal=causal,
                                        smooth_k=True, events=ev, kernel=args.kernel)
-    # the library's choice by size (sage_attn_fwd_ex): 256 queries per block from N = 16384 on
-    q256 = args.kernel == 2 or (args.kernel == 0 and N >= 16384)
+    # the library's choice by size (sage_attn_fwd_ex): 256 queries per block from N = 16384 on,
+    # head_dim 128 only
+    q256 = args.kernel == 2 or (args.kernel == 0 and N >= 16384 and D == 128)
     kname = "attn_fwd_pp_kernel" if q256 else "attn_fwd_kernel"
     for _ in range(args.warmup):
         call()
@@ -220,10 +233,10 @@ def main():
     attn_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
     ev_ms = sum(e[0].elapsed_time(e[2]) for e in evs) / args.steps
 
-    ops = ops_of(B, H, N, causal)
+    ops = ops_of(B, H, N, causal, D)
     value = ops / (ms_step * 1e-3) / 1e12
     attn_tflops = ops / (attn_ms * 1e-3) / 1e12
-    pbytes = prologue_bytes(B, H, N)
+    pbytes = prologue_bytes(B, H, N, D=D)
     pro_gbps = pbytes / (pro_ms * 1e-3) / 1e9
     log("workload %s: %.3f ms/step (events %.3f), prologue %.3f ms (%.0f GB/s), main loop %.3f ms"
         " (%.1f TFLOP/s)" % (args.workload, ms_step, ev_ms, pro_ms, pro_gbps, attn_ms, attn_tflops))
@@ -248,8 +261,8 @@ def main():
         "dtype": "int8" if dt == "fp16" else "fp8",
         "data": "synthetic",
         "pct_mfma_peak": round(100.0 * value / PEAK_TOPS, 2),
-        "config": {"workload": "%s: %s B=%d H=%d N=%d D=128 %s smooth_k %s" % (
-            args.workload, dt, B, H, N, "causal" if causal else "non-causal", layout),
+        "config": {"workload": "%s: %s B=%d H=%d N=%d D=%d %s smooth_k %s" % (
+            args.workload, dt, B, H, N, D, "causal" if causal else "non-causal", layout),
             "global_batch": B, "seq_len": N, "parallelism": "single-gpu"},
         "roofline": {"bound": "mfma", "achieved": round(attn_tflops, 1), "peak": PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(attn_tflops / PEAK_TOPS, 4),

@@ -8,12 +8,13 @@
  * host. Every entry point returns SAGE_OK or a nonzero status; `sage_last_error()` gives the text.
  *
  * Layout vocabulary (the reference's, `sageattention/sk1_backend/sk1_loader.py:405-442`):
- *   Q, K, V, O : logical (B, H, N, D=128) views, element strides (batch, head, row), last stride 1
+ *   Q, K, V, O : logical (B, H, N, D) views, element strides (batch, head, row), last stride 1;
+ *                D (head_dim) is 128, or 64 where an entry point takes D
  *   N_pad      : ceil(N/64)*64
- *   K8         : (B*H, N_pad, 128) int8 (qk_int8) or fp8 e4m3, row-major
+ *   K8         : (B*H, N_pad, D) int8 (qk_int8) or fp8 e4m3, row-major
  *   SK, SV     : (B*H, N_pad) fp32 per-token scales
- *   V8T        : (B*H, 128, N_pad) fp8 e4m3, V transposed
- *   MEAN       : (B*H, 128) fp32 smooth_k mean
+ *   V8T        : (B*H, D, N_pad) fp8 e4m3, V transposed
+ *   MEAN       : (B*H, D) fp32 smooth_k mean
  *   S          : (B*H) fp32 per-(b,h) V-scale fold
  * dtype codes: SAGE_F16 = 0, SAGE_BF16 = 1.
  */
@@ -72,7 +73,10 @@ size_t sage_kv_prologue_workspace_bytes(int64_t BH, int64_t N);
  *             does not produce the mean (`sageattention/sk1_backend/hip_prologue.py:17`).
  *             Costs a third launch (V is read twice).
  *   fold      1: write SV' = SV / S into `sv`; 0: leave SV unfolded (S is written either way)
- *   k, v      logical (B, H, N, 128) views with element strides (k_sb, k_sh, k_sr) / (v_...)
+ *   k, v      logical (B, H, N, D) views with element strides (k_sb, k_sh, k_sr) / (v_...)
+ *   D         head_dim, 64 or 128 (64: no counterpart in the reference's shipped path -- its
+ *             head_dim-64 object `kernels/hip/sk1_d64.hip` is built but never routed,
+ *             `sageattention/sk1_backend/__init__.py:208-229`)
  *   outputs   k8, sk, v8t, sv, s (required); mean (may be NULL; written when smooth_k);
  *             vmean (B*H, 128) fp32 (required with smooth_v, else unused);
  *             kconst (may be NULL): the main loop's per-key constants, (B*H, N_pad/64, 3, 64) fp32:
@@ -84,7 +88,7 @@ size_t sage_kv_prologue_workspace_bytes(int64_t BH, int64_t N);
 int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int smooth_v, int fold,
                      const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sr,
                      const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sr,
-                     int64_t B, int64_t H, int64_t N, int64_t N_pad,
+                     int64_t B, int64_t H, int64_t N, int64_t N_pad, int64_t D,
                      void* k8, float* sk, void* v8t, float* sv, float* mean, float* vmean,
                      float* s, float* kconst, void* workspace, size_t workspace_bytes,
                      void* stream);
@@ -117,7 +121,8 @@ int sage_attn_fwd(int dtype, int qk_int8, int causal,
  * arithmetic in the same order per query; only the block shape and schedule differ. The kernel
  * choice has no counterpart in the reference (one kernel per dtype there).
  *
- *   q, o      logical (B, H, N, 128) views, as in sage_attn_fwd
+ *   q, o      logical (B, H, N, D) views, as in sage_attn_fwd
+ *   D         head_dim, 64 or 128; 64 runs the 128-query kernel (SAGE_KERNEL_Q256 is refused)
  *   k8, kconst, v8t, s   the prologue's outputs for B*H_kv planes of N_kv keys (N_kv_pad =
  *             ceil(N_kv/64)*64). Query head h reads K/V head h / (H / H_kv) (grouped-query and
  *             multi-query attention; H must be a multiple of H_kv), and N may differ from N_kv
@@ -143,19 +148,19 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal,
                      const void* k8, const float* kconst, const void* v8t, const float* s,
                      void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr,
                      int64_t B, int64_t H, int64_t N, int64_t H_kv, int64_t N_kv,
-                     int64_t N_kv_pad, float sm_scale, int kernel,
+                     int64_t N_kv_pad, int64_t D, float sm_scale, int kernel,
                      float* lse, const float* kmean, const float* vmean, void* stream);
 
 /*
  * Q quantization exactly as the main loop performs it, written out for parity checks.
  * Replaces the in-kernel Q quantization of `kernels/hip/sk1_t6i.hip:91-117` (int8) and
  * `kernels/hip/sk1_t4a1s.hip:79-105` (fp8), which the reference never writes out.
- *   q8  (B*H, N, 128) int8 or fp8; sq (B*H, N) fp32 = RN(amax/127) or RN(amax/448);
+ *   q8  (B*H, N, D) int8 or fp8; sq (B*H, N) fp32 = RN(amax/127) or RN(amax/448);
  *   cq  (B*H, N) fp32 = RN(RN(sm_scale*log2e) * sq)
  */
 int sage_quant_q(int dtype, int qk_int8,
                  const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sr,
-                 int64_t B, int64_t H, int64_t N, float sm_scale,
+                 int64_t B, int64_t H, int64_t N, int64_t D, float sm_scale,
                  void* q8, float* sq, float* cq, void* stream);
 
 /*

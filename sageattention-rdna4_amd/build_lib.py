@@ -69,8 +69,23 @@ def build(verbose=False, jobs=None):
     out = lib_path()
     tmp = out + ".tmp"
     _run([HIPCC, "--offload-arch=" + ARCH, "-shared", "-fPIC", "-o", tmp] + objs, verbose)
+    _check_kernel_stubs(tmp)
     os.replace(tmp, out)
     return out
+
+
+def _check_kernel_stubs(lib):
+    """Fail the build if a kernel's host launch stub is undefined. The host pass can drop a kernel
+    template's stub without a diagnostic (a constraint check it cannot satisfy, deferred and never
+    reported), and the library would then link and only fail to load."""
+    nm = os.path.join(os.path.dirname(HIPCC), "..", "lib", "llvm", "bin", "llvm-nm")
+    if not os.path.exists(nm):
+        nm = "nm"
+    res = subprocess.run([nm, "-u", lib], capture_output=True, text=True)
+    missing = [l.split()[-1] for l in res.stdout.splitlines() if "__device_stub__" in l]
+    if missing:
+        raise RuntimeError("undefined kernel stubs in %s (a kernel was dropped by the host pass):\n%s"
+                           % (lib, "\n".join(missing[:8])))
 
 
 if __name__ == "__main__":

@@ -36,7 +36,7 @@
 
 namespace sage {
 
-template <typename T, bool QK_INT8, bool CAUSAL>
+template <typename T, bool QK_INT8, bool CAUSAL, int D>
 __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WAVES, SAGE_ATTN_WAVES))) void attn_fwd_kernel(
     const T* __restrict__ Q, const u8* __restrict__ K8, const float* __restrict__ KC,
     const u8* __restrict__ V8T, const float* __restrict__ Sfold,
@@ -48,9 +48,11 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
   // with the buffer chosen at compile time the compiler can tell a DMA into one buffer from reads
   // of another, and waits for a DMA only where its own buffer is read. (Its wait bookkeeping
   // tells apart a handful of DMA targets, so there are three objects, not nine.)
-  __shared__ StageBuf sB0;
-  __shared__ StageBuf sB1;
-  __shared__ StageBuf sB2;
+  __shared__ StageBuf<D> sB0;
+  __shared__ StageBuf<D> sB1;
+  __shared__ StageBuf<D> sB2;
+  constexpr int NDT = D / 32;   // 32-channel output tiles per wave
+  constexpr int NKV = D / 64;   // 1 KB K and V^T requests per wave and block (each)
 
   // ---- which (plane, q-tile) this block runs ----
   int id = blockIdx.x;
@@ -68,8 +70,8 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
   const int q0 = qt * BM + w * 32;
   const int qrow = q0 + l32;
 
-  const u8* Kb = K8 + (int64_t)kvp * Nk_pad * HD;
-  const u8* Vb = V8T + (int64_t)kvp * HD * Nk_pad;
+  const u8* Kb = K8 + (int64_t)kvp * Nk_pad * D;
+  const u8* Vb = V8T + (int64_t)kvp * D * Nk_pad;
   const float* KCb = KC + (int64_t)kvp * Nk_pad * 3;   // 192 floats per 64-key block
 
   const int n_blocks = Nk_pad / BK;
@@ -80,33 +82,35 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
   // buffers. Block j+2 is requested at the top of block j, and the wait at the bottom of block j
   // covers only block j+1's requests, so a tile has two blocks of compute to arrive (a plane's K/V
   // exceed an XCD's L2: many requests go to the next cache level). Per block every wave issues
-  // exactly five requests: 2 KB of K, 2 KB of V^T and 256 bytes of the per-key constants.
-  //   K:   request I = 2w + i (16 B/lane) carries rows 8I..8I+7; lane l lands at byte 16*l of that
-  //        KB, i.e. row 8I + l/8, chunk slot l%8, which holds logical chunk (l%8) ^ kswz(row).
+  // exactly 2*NKV + 1 requests (five for D = 128, three for D = 64): NKV KB of K, NKV KB of V^T
+  // and 256 bytes of the per-key constants.
+  //   K:   request I = NKV*w + i (16 B/lane) carries the 1024/D rows (1024/D)*I ..; lane l lands
+  //        at byte 16*l of that KB, i.e. row (1024/D)*I + l/(D/16), chunk slot l%(D/16), which
+  //        holds logical chunk slot ^ kswz(row).
   //   V^T: request I carries rows d = 16I..16I+15; lane l -> row 16I + l/4, slot l%4 holding
   //        logical chunk (l%4) ^ vswz(d).
   //   KC:  waves 0..2 carry floats 64w..64w+63 of the block's 192 (4 B/lane); wave 3 repeats
   //        wave 0's into the tile's pad.
-  uint32_t k_off[2], v_off[2];
+  uint32_t k_off[NKV], v_off[NKV];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int I = 2 * w + i;
-    const int krow = 8 * I + (lane >> 3), kpos = lane & 7;
-    k_off[i] = (uint32_t)(krow * HD + 16 * (kpos ^ kswz(krow)));
+  for (int i = 0; i < NKV; ++i) {
+    const int I = NKV * w + i;
+    const int krow = (1024 / D) * I + lane / (D / 16), kpos = lane % (D / 16);
+    k_off[i] = (uint32_t)(krow * D + 16 * (kpos ^ kswz<D>(krow)));
     const int d = 16 * I + (lane >> 2), vpos = lane & 3;
     v_off[i] = (uint32_t)(d * Nk_pad + 16 * (vpos ^ vswz(d)));
   }
   const uint32_t c_off = (uint32_t)(4 * (64 * (w == 3 ? 0 : w) + lane));
   const uint32_t c_dst = (uint32_t)(256 * w);
-  auto dma = [&](int j, StageBuf& buf) {
-    const u8* kblk = Kb + (size_t)(BK * HD) * (uint32_t)j;
+  auto dma = [&](int j, StageBuf<D>& buf) {
+    const u8* kblk = Kb + (size_t)(BK * D) * (uint32_t)j;
     const u8* vblk = Vb + (size_t)BK * (uint32_t)j;
     const u8* cblk = (const u8*)KCb + (size_t)(192 * 4) * (uint32_t)j;
-    const uint32_t kl = lds_addr(buf.k) + 2048 * w, vl = lds_addr(buf.v) + 2048 * w;
-    dma16(kblk, k_off[0], kl);
-    dma16(kblk, k_off[1], kl + 1024);
-    dma16(vblk, v_off[0], vl);
-    dma16(vblk, v_off[1], vl + 1024);
+    const uint32_t kl = lds_addr(buf.k) + 1024 * NKV * w, vl = lds_addr(buf.v) + 1024 * NKV * w;
+#pragma unroll
+    for (int i = 0; i < NKV; ++i) dma16(kblk, k_off[i], kl + 1024 * i);
+#pragma unroll
+    for (int i = 0; i < NKV; ++i) dma16(vblk, v_off[i], vl + 1024 * i);
     dma4(cblk, c_off, lds_addr(&buf.s) + c_dst);
   };
 
@@ -115,17 +119,18 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
   if (j_end > 1) dma(1, sB1);
 
   // ---- Q: per-row quantization straight into MFMA fragments ----
-  QFrag qf;
+  QFrag<D> qf;
   float sq, cq;
   float qmu = 0.0f;   // q . mu for the logsumexp's smooth_k correction (when asked)
-  quant_q_row<T, QK_INT8>(Q + b * q_sb + hd * q_sh + (int64_t)qrow * q_sr, qrow < N, hh, sm_scale,
-                          qf, sq, cq, (LSE && KMEAN) ? KMEAN + (int64_t)kvp * HD : nullptr, &qmu);
+  quant_q_row<T, QK_INT8, D>(Q + b * q_sb + hd * q_sh + (int64_t)qrow * q_sr, qrow < N, hh,
+                             sm_scale, qf, sq, cq,
+                             (LSE && KMEAN) ? KMEAN + (int64_t)kvp * D : nullptr, &qmu);
   (void)sq;
   const float Sb = Sfold[kvp];
 
-  f32x16 acc[4];
+  f32x16 acc[NDT];
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[dt][r] = 0.0f;
   float m_x = -INFINITY;     // running max of x = (Q8.K8)*SK for this lane's query
@@ -133,7 +138,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
   float l_i = 0.0f;
 
   const int krow0 = kappa(0, l32), krow1 = kappa(1, l32);
-  const int ksw0 = kswz(krow0), ksw1 = kswz(krow1);
+  const int ksw0 = kswz<D>(krow0), ksw1 = kswz<D>(krow1);
   const int vrow = l32;               // + 32 dt
   const int vsw = vswz(vrow);         // vswz(32dt + r) == vswz(r)
 
@@ -144,13 +149,14 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
   // compiler can tell the requests in flight to other buffers from this block's reads). At the
   // top: request block j+2 into buffer (P+2) % 3, which block j-1 read and every wave has
   // finished with (barrier). At the bottom: wait until this wave's requests for block j+1 have
-  // landed (five requests per block, in order: vmcnt(5) leaves just block j+2's), then barrier.
+  // landed (2*NKV + 1 requests per block, in order: vmcnt(2*NKV + 1) leaves just block j+2's),
+  // then barrier.
   // The barrier is written as asm with a memory clobber: a workgroup fence would also wait for
   // block j+2's requests.
   auto block = [&](const int j, auto par) {
     constexpr int P = decltype(par)::value;
-    StageBuf& bcur = P == 0 ? sB0 : (P == 1 ? sB1 : sB2);
-    StageBuf& bnew = P == 0 ? sB2 : (P == 1 ? sB0 : sB1);
+    StageBuf<D>& bcur = P == 0 ? sB0 : (P == 1 ? sB1 : sB2);
+    StageBuf<D>& bnew = P == 0 ? sB2 : (P == 1 ? sB0 : sB1);
     const u8* const kcur = bcur.k;
     const u8* const vcur = bcur.v;
     const ScaleTile& sc = bcur.s;
@@ -160,13 +166,13 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
     if (!CAUSAL || j < w_end) {
       const KeyConsts kc = load_key_consts(sc, lane);
       f32x16 st[2];
-      qk_block<QK_INT8>(kcur, qf, krow0, krow1, ksw0, ksw1, hh, st);
+      qk_block<QK_INT8, D>(kcur, qf, krow0, krow1, ksw0, ksw1, hh, st);
       i32x8 pb;
       softmax_block<QK_INT8, CAUSAL>(st, kc, j, q0, qrow, Nk, hh, cq, m_x, mc, l_i, acc, pb);
 
       // ---------- O^T += V^T . P^T ----------
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
+      for (int dt = 0; dt < NDT; ++dt) {
         const u8* vb = &vcur[(32 * dt + vrow) * BK];
         const i32x4 lo = *(const i32x4*)(vb + 16 * ((2 * hh) ^ vsw));
         const i32x4 hi = *(const i32x4*)(vb + 16 * ((2 * hh + 1) ^ vsw));
@@ -175,9 +181,12 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
       }
     }
 
-    if (more2)
-      asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else
+    if (more2) {
+      if constexpr (NKV == 2)
+        asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    } else
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   };
   for (int j = 0; j < j_end; j += 3) {
@@ -188,16 +197,16 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
   // acc is read below only inside the divergent `qrow < N` branch; keep the loop's MFMAs out
   // of it (an MFMA under a partial EXEC mask loses the inactive lanes' operand rows).
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt) asm volatile("" ::"v"(acc[dt]));
+  for (int dt = 0; dt < NDT; ++dt) keep_live(acc[dt]);
 
   // ---------- epilogue: O = acc * S / (l * 448) (+ V's mean with smooth_v, one fma) ----------
   if (qrow < N) {
     if (LSE && hh == 0) LSE[(int64_t)bh * N + qrow] = row_lse(mc, l_i, sm_scale, qmu);
     const float inv = (l_i > 0.0f) ? __fdiv_rn(Sb, l_i * P_SCALE) : 0.0f;
     T* op = O + b * o_sb + hd * o_sh + (int64_t)qrow * o_sr;
-    const float* vmp = VMEAN ? VMEAN + (int64_t)kvp * HD : nullptr;
+    const float* vmp = VMEAN ? VMEAN + (int64_t)kvp * D : nullptr;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d = 32 * dt + 8 * g + 4 * hh;
@@ -223,7 +232,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WA
 // Parity entry: Q quantization exactly as the main loop does it, written out.
 // grid (ceil(N/32), BH), block 64: lane (q, h) of the wave handles row 32*blockIdx.x + q.
 // ---------------------------------------------------------------------------------------------
-template <typename T, bool QK_INT8>
+template <typename T, bool QK_INT8, int D>
 __global__ __launch_bounds__(64) void quant_q_kernel(const T* __restrict__ Q, int64_t q_sb,
                                                      int64_t q_sh, int64_t q_sr, int H, int N,
                                                      float sm_scale, u8* __restrict__ Q8,
@@ -231,18 +240,18 @@ __global__ __launch_bounds__(64) void quant_q_kernel(const T* __restrict__ Q, in
   const int bh = blockIdx.y, b = bh / H, hd = bh - b * H;
   const int lane = threadIdx.x, l32 = lane & 31, hh = lane >> 5;
   const int qrow = blockIdx.x * 32 + l32;
-  QFrag qf;
+  QFrag<D> qf;
   float sq, cq;
-  quant_q_row<T, QK_INT8>(Q + b * q_sb + hd * q_sh + (int64_t)qrow * q_sr, qrow < N, hh, sm_scale,
-                          qf, sq, cq);
+  quant_q_row<T, QK_INT8, D>(Q + b * q_sb + hd * q_sh + (int64_t)qrow * q_sr, qrow < N, hh,
+                             sm_scale, qf, sq, cq);
   if (qrow >= N) return;
-  u8* dst = Q8 + ((int64_t)bh * N + qrow) * HD;
+  u8* dst = Q8 + ((int64_t)bh * N + qrow) * D;
   if (QK_INT8) {
 #pragma unroll
-    for (int dd = 0; dd < 4; ++dd) *(i32x4*)(dst + 32 * dd + 16 * hh) = qf.i8[dd];
+    for (int dd = 0; dd < D / 32; ++dd) *(i32x4*)(dst + 32 * dd + 16 * hh) = qf.i8[dd];
   } else {
 #pragma unroll
-    for (int dd = 0; dd < 2; ++dd) {
+    for (int dd = 0; dd < D / 64; ++dd) {
       const i32x8 v = qf.f8[dd];
       *(i32x4*)(dst + 64 * dd + 32 * hh) = (i32x4){v[0], v[1], v[2], v[3]};
       *(i32x4*)(dst + 64 * dd + 32 * hh + 16) = (i32x4){v[4], v[5], v[6], v[7]};
@@ -287,17 +296,26 @@ __global__ __launch_bounds__(64) void layout_probe_kernel(const u8* __restrict__
 }
 
 // ---------------------------------------------------------------------------------------------
-template <typename T, bool QK_INT8, bool CAUSAL>
-static void launch_attn_t(const AttnArgs& a, hipStream_t stream) {
+template <typename T, bool QK_INT8, bool CAUSAL, int D>
+static void launch_attn_d(const AttnArgs& a, hipStream_t stream) {
   const int BH = (int)(a.B * a.H);
   const int num_qt = (int)((a.N + BM - 1) / BM);
   const int total = num_qt * BH;
   const int span = (total / 8) * 8;
-  hipLaunchKernelGGL((attn_fwd_kernel<T, QK_INT8, CAUSAL>), dim3(total), dim3(AT), 0, stream,
+  hipLaunchKernelGGL((attn_fwd_kernel<T, QK_INT8, CAUSAL, D>), dim3(total), dim3(AT), 0, stream,
                      (const T*)a.q, (const u8*)a.k8, a.kconst, (const u8*)a.v8t, a.s, (T*)a.o,
                      a.q_sb, a.q_sh, a.q_sr, a.o_sb, a.o_sh, a.o_sr, (int)a.H, (int)a.H_kv,
                      (int)(a.H / a.H_kv), (int)a.N, (int)a.N_kv, (int)a.N_kv_pad, num_qt, span,
                      a.sm_scale, a.lse, a.kmean, a.vmean);
+}
+
+template <typename T, bool QK_INT8, bool CAUSAL>
+static void launch_attn_t(const AttnArgs& a, hipStream_t stream) {
+  if (a.D == 64) {
+    launch_attn_d<T, QK_INT8, CAUSAL, 64>(a, stream);
+  } else {
+    launch_attn_d<T, QK_INT8, CAUSAL, 128>(a, stream);
+  }
 }
 
 hipError_t launch_attn_fwd(const AttnArgs& a, hipStream_t stream) {
@@ -320,20 +338,29 @@ hipError_t launch_attn_fwd(const AttnArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_quant_q(const QuantQArgs& a, hipStream_t stream) {
+template <typename T, bool QK_INT8, int D>
+static void launch_quant_q_t(const QuantQArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)((a.N + 31) / 32), (unsigned)(a.B * a.H));
+  hipLaunchKernelGGL((quant_q_kernel<T, QK_INT8, D>), grid, dim3(64), 0, stream, (const T*)a.q,
+                     a.q_sb, a.q_sh, a.q_sr, (int)a.H, (int)a.N, a.sm_scale, (u8*)a.q8, a.sq,
+                     a.cq);
+}
+
+template <int D>
+static void launch_quant_q_d(const QuantQArgs& a, hipStream_t stream) {
   if (a.dtype == 1)
-    hipLaunchKernelGGL((quant_q_kernel<bf16, false>), grid, dim3(64), 0, stream,
-                       (const bf16*)a.q, a.q_sb, a.q_sh, a.q_sr, (int)a.H, (int)a.N, a.sm_scale,
-                       (u8*)a.q8, a.sq, a.cq);
+    launch_quant_q_t<bf16, false, D>(a, stream);
   else if (a.qk_int8)
-    hipLaunchKernelGGL((quant_q_kernel<f16, true>), grid, dim3(64), 0, stream, (const f16*)a.q,
-                       a.q_sb, a.q_sh, a.q_sr, (int)a.H, (int)a.N, a.sm_scale, (u8*)a.q8, a.sq,
-                       a.cq);
+    launch_quant_q_t<f16, true, D>(a, stream);
   else
-    hipLaunchKernelGGL((quant_q_kernel<f16, false>), grid, dim3(64), 0, stream, (const f16*)a.q,
-                       a.q_sb, a.q_sh, a.q_sr, (int)a.H, (int)a.N, a.sm_scale, (u8*)a.q8, a.sq,
-                       a.cq);
+    launch_quant_q_t<f16, false, D>(a, stream);
+}
+
+hipError_t launch_quant_q(const QuantQArgs& a, hipStream_t stream) {
+  if (a.D == 64)
+    launch_quant_q_d<64>(a, stream);
+  else
+    launch_quant_q_d<128>(a, stream);
   return hipGetLastError();
 }
 

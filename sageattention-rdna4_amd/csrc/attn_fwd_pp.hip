@@ -38,7 +38,7 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
     int N, int Nk, int Nk_pad, int num_qt, int xcd_span, float sm_scale,
     float* __restrict__ LSE, const float* __restrict__ KMEAN,
     const float* __restrict__ VMEAN) {
-  __shared__ StageBuf sB[3];
+  __shared__ StageBuf<HD> sB[3];
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
@@ -79,10 +79,10 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
   // block j's tiles into buffer p: K (one request per wave), then V^T and constants (one or two).
   // The block offset goes into the per-lane 32-bit offset, so the 64-bit bases stay fixed.
   auto dma_k = [&](int j, int p) {
-    dma16(Kb, k_off + (uint32_t)(BK * HD) * (uint32_t)j, lds0 + (uint32_t)p * (uint32_t)sizeof(StageBuf));
+    dma16(Kb, k_off + (uint32_t)(BK * HD) * (uint32_t)j, lds0 + (uint32_t)p * (uint32_t)sizeof(StageBuf<HD>));
   };
   auto dma_vc = [&](int j, int p) {
-    const uint32_t base = lds0 + (uint32_t)p * (uint32_t)sizeof(StageBuf);
+    const uint32_t base = lds0 + (uint32_t)p * (uint32_t)sizeof(StageBuf<HD>);
     dma16(Vb, v_off + (uint32_t)BK * (uint32_t)j, base + BK * HD);
     if (w < 3) dma4(KCb, c_off + (uint32_t)(192 * 4) * (uint32_t)j, base + 2 * BK * HD - 768 * w);
   };
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
   }
 
   // ---- Q: per-row quantization straight into MFMA fragments ----
-  QFrag qf;
+  QFrag<HD> qf;
   float sq, cq;
   float qmu = 0.0f;   // q . mu for the logsumexp's smooth_k correction (when asked)
   quant_q_row<T, QK_INT8>(Q + b * q_sb + hd * q_sh + (int64_t)qrow * q_sr, qrow < N, hh, sm_scale,

@@ -61,6 +61,12 @@ int check_shape(int64_t B, int64_t H, int64_t N, int64_t N_pad) {
   return SAGE_OK;
 }
 
+int check_head_dim(int64_t D) {
+  if (D != 64 && D != 128)
+    return fail(SAGE_ERR_INVALID, "head_dim: D must be 64 or 128 (got %lld)", (long long)D);
+  return SAGE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -77,7 +83,8 @@ size_t sage_kv_prologue_workspace_bytes(int64_t BH, int64_t N) {
 int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int smooth_v, int fold, const void* k,
                      int64_t k_sb, int64_t k_sh, int64_t k_sr, const void* v, int64_t v_sb,
                      int64_t v_sh, int64_t v_sr, int64_t B, int64_t H, int64_t N, int64_t N_pad,
-                     void* k8, float* sk, void* v8t, float* sv, float* mean, float* vmean,
+                     int64_t D, void* k8, float* sk, void* v8t, float* sv, float* mean,
+                     float* vmean,
                      float* s, float* kconst, void* workspace, size_t workspace_bytes,
                      void* stream) {
   if (dtype != SAGE_F16 && dtype != SAGE_BF16)
@@ -86,6 +93,7 @@ int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int smooth_v, int fold
     return fail(SAGE_ERR_INVALID, "bf16_int8: int8 K is served for fp16 inputs only");
   int rc = check_shape(B, H, N, N_pad);
   if (rc) return rc;
+  if ((rc = check_head_dim(D))) return rc;
   if ((rc = check_view("k", k, k_sb, k_sh, k_sr))) return rc;
   if ((rc = check_view("v", v, v_sb, v_sh, v_sr))) return rc;
   if (!k8 || !sk || !v8t || !sv || !s) return fail(SAGE_ERR_INVALID, "an output pointer is NULL");
@@ -115,6 +123,7 @@ int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int smooth_v, int fold
   a.H = H;
   a.N = N;
   a.N_pad = N_pad;
+  a.D = D;
   a.k8 = k8;
   a.sk = sk;
   a.v8t = v8t;
@@ -131,7 +140,7 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
                      int64_t q_sh, int64_t q_sr, const void* k8, const float* kconst,
                      const void* v8t, const float* s, void* o, int64_t o_sb, int64_t o_sh,
                      int64_t o_sr, int64_t B, int64_t H, int64_t N, int64_t H_kv, int64_t N_kv,
-                     int64_t N_kv_pad, float sm_scale, int kernel, float* lse,
+                     int64_t N_kv_pad, int64_t D, float sm_scale, int kernel, float* lse,
                      const float* kmean, const float* vmean, void* stream) {
   if (dtype != SAGE_F16 && dtype != SAGE_BF16)
     return fail(SAGE_ERR_INVALID, "dtype: unsupported dtype code %d", dtype);
@@ -146,6 +155,9 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
   if (causal && N != N_kv)
     return fail(SAGE_ERR_INVALID, "seq_len: causal attention needs N == N_kv (N=%lld N_kv=%lld)",
                 (long long)N, (long long)N_kv);
+  if ((rc = check_head_dim(D))) return rc;
+  if (D == 64 && kernel == SAGE_KERNEL_Q256)
+    return fail(SAGE_ERR_INVALID, "kernel: the 256-query kernel serves head_dim 128 only");
   if ((rc = check_view("q", q, q_sb, q_sh, q_sr))) return rc;
   if ((rc = check_view("o", o, o_sb, o_sh, o_sr))) return rc;
   if (!k8 || !kconst || !v8t || !s) return fail(SAGE_ERR_INVALID, "an input pointer is NULL");
@@ -183,6 +195,7 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
   a.H_kv = H_kv;
   a.N_kv = N_kv;
   a.N_kv_pad = N_kv_pad;
+  a.D = D;
   a.sm_scale = sm_scale;
   a.lse = lse;
   a.kmean = lse ? kmean : nullptr;
@@ -190,7 +203,7 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
   // The 256-query ping-pong pays off on long sequences; at short ones its larger tiles leave too
   // few blocks per CU and more causal diagonal work, and the 128-query kernel is as fast or faster.
   const bool q256 = kernel == SAGE_KERNEL_Q256 ||
-                    (kernel == SAGE_KERNEL_AUTO && N >= 16384 && N_kv >= 16384);
+                    (kernel == SAGE_KERNEL_AUTO && D == 128 && N >= 16384 && N_kv >= 16384);
   return hip_status(q256 ? sage::launch_attn_fwd_pp(a, (hipStream_t)stream)
                          : sage::launch_attn_fwd(a, (hipStream_t)stream),
                     "sage_attn_fwd launch");
@@ -201,19 +214,20 @@ int sage_attn_fwd(int dtype, int qk_int8, int causal, const void* q, int64_t q_s
                   const float* s, void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr, int64_t B,
                   int64_t H, int64_t N, int64_t N_pad, float sm_scale, void* stream) {
   return sage_attn_fwd_ex(dtype, qk_int8, causal, q, q_sb, q_sh, q_sr, k8, kconst, v8t, s, o,
-                          o_sb, o_sh, o_sr, B, H, N, H, N, N_pad, sm_scale, SAGE_KERNEL_AUTO,
-                          nullptr, nullptr, nullptr, stream);
+                          o_sb, o_sh, o_sr, B, H, N, H, N, N_pad, 128, sm_scale,
+                          SAGE_KERNEL_AUTO, nullptr, nullptr, nullptr, stream);
 }
 
 int sage_quant_q(int dtype, int qk_int8, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sr,
-                 int64_t B, int64_t H, int64_t N, float sm_scale, void* q8, float* sq, float* cq,
-                 void* stream) {
+                 int64_t B, int64_t H, int64_t N, int64_t D, float sm_scale, void* q8, float* sq,
+                 float* cq, void* stream) {
   if (dtype != SAGE_F16 && dtype != SAGE_BF16)
     return fail(SAGE_ERR_INVALID, "dtype: unsupported dtype code %d", dtype);
   if (dtype == SAGE_BF16 && qk_int8)
     return fail(SAGE_ERR_INVALID, "bf16_int8: int8 Q is served for fp16 inputs only");
   int rc = check_shape(B, H, N, (N + 63) / 64 * 64);
   if (rc) return rc;
+  if ((rc = check_head_dim(D))) return rc;
   if ((rc = check_view("q", q, q_sb, q_sh, q_sr))) return rc;
   if (!q8 || !sq || !cq) return fail(SAGE_ERR_INVALID, "an output pointer is NULL");
   if (!aligned16(q8)) return fail(SAGE_ERR_INVALID, "ptr_align: q8 must be 16-byte aligned");
@@ -227,6 +241,7 @@ int sage_quant_q(int dtype, int qk_int8, const void* q, int64_t q_sb, int64_t q_
   a.B = B;
   a.H = H;
   a.N = N;
+  a.D = D;
   a.sm_scale = sm_scale;
   a.q8 = q8;
   a.sq = sq;

@@ -27,15 +27,25 @@
 namespace sage {
 
 constexpr int PT = 256;          // threads per block
-constexpr int STEP = 128;        // rows per stats step (one V8T tile)
-constexpr int VT_STRIDE = 144;   // LDS bytes per transposed-V row (128 tokens + 16 pad)
 
-PrologueGeom prologue_geom(int64_t BH, int64_t N_pad) {
+// Thread layout of both passes for head_dim D: CG = D/8 column groups of 8 columns (one 16-byte
+// load) x RG = 256/CG row groups; a row's CG lanes are one aligned CG-lane group of a wave. The
+// stats pass moves STEP = 8*RG rows per step (8 consecutive tokens per thread: one 8-byte word of
+// the transposed tile per column), through an LDS tile of D rows x (STEP + 16) bytes.
+template <int D>
+struct Geo {
+  static constexpr int CG = D / 8, RG = PT / CG, STEP = 8 * RG, VTS = STEP + 16;
+};
+
+PrologueGeom prologue_geom(int64_t BH, int64_t N_pad, int64_t step) {
   auto clampr = [](int64_t x, int64_t lo, int64_t hi) { return x < lo ? lo : (x > hi ? hi : x); };
   auto up128 = [](int64_t x) { return (x + 127) / 128 * 128; };
   PrologueGeom g;
-  // Aim for ~1024 stats blocks and ~2048 quant blocks on big calls.
-  g.R1 = clampr(up128((N_pad * BH + 1023) / 1024), 128, 2048);
+  // Aim for ~1024 stats blocks and ~2048 quant blocks on big calls. A stats block's rows are a
+  // whole number of its steps (128 rows for head_dim 128, 256 for 64), so no step reaches into
+  // the next block's rows; a larger step only lowers C1, so the head_dim-128 geometry bounds the
+  // workspace for both.
+  g.R1 = clampr((((N_pad * BH + 1023) / 1024) + step - 1) / step * step, step, 2048);
   g.C1 = (N_pad + g.R1 - 1) / g.R1;
   g.R2 = clampr(up128((N_pad * BH + 2047) / 2048), 128, 1024);
   g.C2 = (N_pad + g.R2 - 1) / g.R2;
@@ -56,9 +66,9 @@ size_t prologue_workspace_bytes(int64_t BH, int64_t N_pad) {
 
 // ---------------------------------------------------------------------------------------------
 // Stats pass. grid (C1, BH), block 256.
-// In a 128-row step, thread (cg, rg) owns rows 8rg .. 8rg+7 and columns 8cg .. 8cg+7, so for each
+// In a STEP-row step, thread (cg, rg) owns rows 8rg .. 8rg+7 and columns 8cg .. 8cg+7, so for each
 // of its 8 columns it holds 8 consecutive tokens: one 8-byte word of the transposed tile. The LDS
-// tile is [128 d][144 B]; the 8-byte chunk of tokens 8rg..8rg+7 of row d sits at chunk position
+// tile is [D d][STEP+16 B]; the 8-byte chunk of tokens 8rg..8rg+7 of row d sits at chunk position
 // rg ^ (d >> 3), which keeps both the column writes and the row reads free of bank conflicts.
 // ---------------------------------------------------------------------------------------------
 // V_QUANT: V quantized as it is (and K's mean partials when smooth_k) -- the whole stats pass.
@@ -67,23 +77,25 @@ size_t prologue_workspace_bytes(int64_t BH, int64_t N_pad) {
 //             launch; K is not read).
 enum VMode { V_QUANT = 0, V_SUMS = 1, V_CENTERED = 2 };
 
-template <typename T, int VMODE>
+template <typename T, int VMODE, int D>
 __global__ __launch_bounds__(PT) void kv_stats_kernel(
     const T* __restrict__ K, const T* __restrict__ V, u8* __restrict__ V8T, float* __restrict__ SV,
     double* __restrict__ part, double* __restrict__ vpart, float* __restrict__ VMEAN,
     float* __restrict__ smax, int64_t H, int64_t N, int64_t N_pad, int64_t R1, int64_t C1,
     int64_t k_sb, int64_t k_sh, int64_t k_sr, int64_t v_sb, int64_t v_sh, int64_t v_sr,
     int smooth_k) {
-  __shared__ __attribute__((aligned(16))) u8 tile[HD * VT_STRIDE];
+  using G = Geo<D>;
+  constexpr int STEP = G::STEP, VT_STRIDE = G::VTS, RG = G::RG;
+  __shared__ __attribute__((aligned(16))) u8 tile[D * VT_STRIDE];
   __shared__ float wmax[PT / 64];
-  __shared__ float vmu_s[HD];
+  __shared__ float vmu_s[D];
 
-  const int tid = threadIdx.x, cg = tid & 15, rg = tid >> 4;
+  const int tid = threadIdx.x, cg = tid % G::CG, rg = tid / G::CG;
   const int64_t c = blockIdx.x, bh = blockIdx.y;
   const int64_t b = bh / H, h = bh - b * H;
   const T* kp = K + b * k_sb + h * k_sh + 8 * cg;
   const T* vp = V + b * v_sb + h * v_sh + 8 * cg;
-  u8* vt = V8T + bh * HD * N_pad;
+  u8* vt = V8T + bh * D * N_pad;
   const int64_t r_begin = c * R1;
   const int64_t r_end = (r_begin + R1 < N_pad) ? r_begin + R1 : N_pad;
   const bool k_sums = smooth_k && VMODE != V_CENTERED;
@@ -92,12 +104,12 @@ __global__ __launch_bounds__(PT) void kv_stats_kernel(
   // same order, so all of them subtract the same bits.
   float vmu[8];
   if (VMODE == V_CENTERED) {
-    if (tid < HD) {
+    if (tid < D) {
       double sum = 0.0;
-      for (int64_t cc = 0; cc < C1; ++cc) sum += vpart[(bh * C1 + cc) * HD + tid];
+      for (int64_t cc = 0; cc < C1; ++cc) sum += vpart[(bh * C1 + cc) * D + tid];
       const float m = (float)(sum / (double)N);
       vmu_s[tid] = m;
-      if (c == 0) VMEAN[bh * HD + tid] = m;
+      if (c == 0) VMEAN[bh * D + tid] = m;
     }
     __syncthreads();
 #pragma unroll
@@ -155,7 +167,7 @@ __global__ __launch_bounds__(PT) void kv_stats_kernel(
       float vmax = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) vmax = fmaxf(vmax, fabsf(f[e]));
-      vmax = max16(vmax);
+      vmax = maxg<G::CG>(vmax);
       const float sv = fmaxf(__fdiv_rn(vmax, P_SCALE), SCALE_FLOOR);
       if (cg == 0 && n < N_pad) SV[bh * N_pad + n] = live ? sv : 0.0f;
       if (live) sv_max = fmaxf(sv_max, sv);
@@ -176,12 +188,14 @@ __global__ __launch_bounds__(PT) void kv_stats_kernel(
     }
     __syncthreads();
     {
-      const int d = tid >> 1, half = tid & 1, dx = d >> 3;
-      const int64_t nb = n0 + 64 * half;
+      // PT/D threads per row d, 64 tokens (4 x 16 bytes) each
+      constexpr int TPD = PT / D;
+      const int d = tid / TPD, part = tid % TPD, dx = d >> 3;
+      const int64_t nb = n0 + 64 * part;
       if (nb < N_pad) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          const int r0 = 8 * half + 2 * m;  // token chunks r0, r0+1 (8 tokens each)
+          const int r0 = 8 * part + 2 * m;  // token chunks r0, r0+1 (8 tokens each)
           const int p0 = r0 ^ dx;
           u32x4 x = *(const u32x4*)(tile + d * VT_STRIDE + 8 * (p0 & ~1));
           if (p0 & 1) x = (u32x4){x.z, x.w, x.x, x.y};
@@ -192,29 +206,30 @@ __global__ __launch_bounds__(PT) void kv_stats_kernel(
     __syncthreads();
   }
 
-  // fp64 mean partials: reduce the 16 row groups in a fixed order.
-  double* red = (double*)tile;  // 16 x 128 doubles = 16 KB <= sizeof(tile)
+  // fp64 mean partials: reduce the RG row groups in a fixed order.
+  static_assert(RG * D * sizeof(double) <= sizeof(tile), "reduction buffer");
+  double* red = (double*)tile;  // RG x D doubles = 16 KB
   if (k_sums) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) red[rg * HD + 8 * cg + e] = ks[e];
+    for (int e = 0; e < 8; ++e) red[rg * D + 8 * cg + e] = ks[e];
     __syncthreads();
-    if (tid < HD) {
+    if (tid < D) {
       double s = 0.0;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s += red[r * HD + tid];
-      part[(bh * C1 + c) * HD + tid] = s;
+      for (int r = 0; r < RG; ++r) s += red[r * D + tid];
+      part[(bh * C1 + c) * D + tid] = s;
     }
     __syncthreads();
   }
   if (VMODE == V_SUMS) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) red[rg * HD + 8 * cg + e] = vs[e];
+    for (int e = 0; e < 8; ++e) red[rg * D + 8 * cg + e] = vs[e];
     __syncthreads();
-    if (tid < HD) {
+    if (tid < D) {
       double s = 0.0;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s += red[r * HD + tid];
-      vpart[(bh * C1 + c) * HD + tid] = s;
+      for (int r = 0; r < RG; ++r) s += red[r * D + tid];
+      vpart[(bh * C1 + c) * D + tid] = s;
     }
     return;   // V is quantized by the V_CENTERED launch
   }
@@ -230,31 +245,33 @@ __global__ __launch_bounds__(PT) void kv_stats_kernel(
 // ---------------------------------------------------------------------------------------------
 // Quant pass. grid (C2, BH), block 256. Thread (cg, rg) handles row base+rg+16i, columns 8cg..+7.
 // ---------------------------------------------------------------------------------------------
-template <typename T, bool KINT8>
+template <typename T, bool KINT8, int D>
 __global__ __launch_bounds__(PT) void k_quant_kernel(
     const T* __restrict__ K, u8* __restrict__ K8, float* __restrict__ SK, float* __restrict__ SV,
     const double* __restrict__ part, const float* __restrict__ smax, float* __restrict__ MEAN,
     float* __restrict__ S_out, float* __restrict__ KC, int64_t H, int64_t N, int64_t N_pad,
     int64_t R2, int64_t C1,
     int64_t k_sb, int64_t k_sh, int64_t k_sr, int smooth_k, int fold) {
-  __shared__ float mu_s[HD];
+  using G = Geo<D>;
+  constexpr int RG = G::RG;
+  __shared__ float mu_s[D];
   __shared__ float s_fold;
 
-  const int tid = threadIdx.x, cg = tid & 15, rg = tid >> 4;
+  const int tid = threadIdx.x, cg = tid % G::CG, rg = tid / G::CG;
   const int64_t bh = blockIdx.y;
   const int64_t b = bh / H, h = bh - b * H;
 
-  if (tid < HD) {
+  if (tid < D) {
     float mu = 0.0f;
     if (smooth_k) {
       double s = 0.0;
-      for (int64_t c = 0; c < C1; ++c) s += part[(bh * C1 + c) * HD + tid];
+      for (int64_t c = 0; c < C1; ++c) s += part[(bh * C1 + c) * D + tid];
       mu = (float)(s / (double)N);
-      if (MEAN != nullptr && blockIdx.x == 0) MEAN[bh * HD + tid] = mu;
+      if (MEAN != nullptr && blockIdx.x == 0) MEAN[bh * D + tid] = mu;
     }
     mu_s[tid] = mu;
-  } else if (tid < HD + 64) {
-    const int l = tid - HD;
+  } else if (tid < D + 64) {
+    const int l = tid - D;
     float m = 1.0f;
     for (int64_t c = l; c < C1; c += 64) m = fmaxf(m, smax[bh * C1 + c]);
 #pragma unroll
@@ -275,15 +292,16 @@ __global__ __launch_bounds__(PT) void k_quant_kernel(
   const int64_t r_end = (r_begin + R2 < N_pad) ? r_begin + R2 : N_pad;
 
   for (int64_t n0 = r_begin; n0 < r_end; n0 += 64) {
-    u32x4 kw[4];
+    // 64 rows per step: rows n0 + rg + RG*i
+    u32x4 kw[64 / RG];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t n = n0 + rg + 16 * i;
+    for (int i = 0; i < 64 / RG; ++i) {
+      const int64_t n = n0 + rg + RG * i;
       kw[i] = (n < N) ? *(const u32x4*)(kp + n * k_sr) : (u32x4){0u, 0u, 0u, 0u};
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t n = n0 + rg + 16 * i;
+    for (int i = 0; i < 64 / RG; ++i) {
+      const int64_t n = n0 + rg + RG * i;
       const bool live = n < N;
       float kc[8];
       unpack8<T>(kw[i], kc);
@@ -293,7 +311,7 @@ __global__ __launch_bounds__(PT) void k_quant_kernel(
         kc[e] = live ? (smooth_k ? kc[e] - mu[e] : kc[e]) : 0.0f;
         kmax = fmaxf(kmax, fabsf(kc[e]));
       }
-      kmax = max16(kmax);
+      kmax = maxg<G::CG>(kmax);
       const float sk = fmaxf(__fdiv_rn(kmax, KINT8 ? I8_MAX : P_SCALE), SCALE_FLOOR);
       if (n < r_end) {
         u32x2 word;
@@ -308,7 +326,7 @@ __global__ __launch_bounds__(PT) void k_quant_kernel(
           for (int e = 0; e < 8; ++e) x[e] = fminf(__fdiv_rn(kc[e], sk), P_SCALE);
           word = (u32x2){fp8x4(x[0], x[1], x[2], x[3]), fp8x4(x[4], x[5], x[6], x[7])};
         }
-        *(u32x2*)(K8 + (bh * N_pad + n) * HD + 8 * cg) = word;
+        *(u32x2*)(K8 + (bh * N_pad + n) * D + 8 * cg) = word;
         // The main loop's per-key constants of 64-key block n/64 (KC, optional): SK, the fma
         // addend -RN(1.5*2^23*SK) (0 for e4m3 K) and RN(SV'*448), 64 floats each.
         float* kc = KC ? KC + (bh * (N_pad / 64) + n / 64) * 192 + (n & 63) : nullptr;
@@ -331,29 +349,30 @@ __global__ __launch_bounds__(PT) void k_quant_kernel(
   }
 }
 
-template <typename T>
+template <typename T, int D>
 static hipError_t launch_prologue_t(const PrologueArgs& a, hipStream_t stream) {
   const int64_t BH = a.B * a.H;
-  const PrologueGeom g = prologue_geom(BH, a.N_pad);
-  const size_t part_bytes = part_region_bytes(BH, g);
+  const PrologueGeom g = prologue_geom(BH, a.N_pad, Geo<D>::STEP);
+  // region offsets as sized for head_dim 128 (prologue_workspace_bytes)
+  const size_t part_bytes = part_region_bytes(BH, prologue_geom(BH, a.N_pad));
   double* part = (double*)a.workspace;
   double* vpart = (double*)((char*)a.workspace + part_bytes);
   float* smax = (float*)((char*)a.workspace + 2 * part_bytes);
   const dim3 grid1((unsigned)g.C1, (unsigned)BH);
   if (a.smooth_v) {
     // V's mean first (with K's partials), then V - mean quantized
-    hipLaunchKernelGGL((kv_stats_kernel<T, V_SUMS>), grid1, dim3(PT), 0, stream, (const T*)a.k,
+    hipLaunchKernelGGL((kv_stats_kernel<T, V_SUMS, D>), grid1, dim3(PT), 0, stream, (const T*)a.k,
                        (const T*)a.v, (u8*)a.v8t, a.sv, part, vpart, a.vmean, smax, a.H, a.N,
                        a.N_pad, g.R1, g.C1, a.k_sb, a.k_sh, a.k_sr, a.v_sb, a.v_sh, a.v_sr,
                        a.smooth_k);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((kv_stats_kernel<T, V_CENTERED>), grid1, dim3(PT), 0, stream,
+    hipLaunchKernelGGL((kv_stats_kernel<T, V_CENTERED, D>), grid1, dim3(PT), 0, stream,
                        (const T*)a.k, (const T*)a.v, (u8*)a.v8t, a.sv, part, vpart, a.vmean, smax,
                        a.H, a.N, a.N_pad, g.R1, g.C1, a.k_sb, a.k_sh, a.k_sr, a.v_sb, a.v_sh,
                        a.v_sr, a.smooth_k);
   } else {
-    hipLaunchKernelGGL((kv_stats_kernel<T, V_QUANT>), grid1, dim3(PT), 0, stream, (const T*)a.k,
+    hipLaunchKernelGGL((kv_stats_kernel<T, V_QUANT, D>), grid1, dim3(PT), 0, stream, (const T*)a.k,
                        (const T*)a.v, (u8*)a.v8t, a.sv, part, vpart, a.vmean, smax, a.H, a.N,
                        a.N_pad, g.R1, g.C1, a.k_sb, a.k_sh, a.k_sr, a.v_sb, a.v_sh, a.v_sr,
                        a.smooth_k);
@@ -361,18 +380,22 @@ static hipError_t launch_prologue_t(const PrologueArgs& a, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (a.k_int8)
-    hipLaunchKernelGGL((k_quant_kernel<T, true>), dim3((unsigned)g.C2, (unsigned)BH), dim3(PT), 0,
+    hipLaunchKernelGGL((k_quant_kernel<T, true, D>), dim3((unsigned)g.C2, (unsigned)BH), dim3(PT), 0,
                        stream, (const T*)a.k, (u8*)a.k8, a.sk, a.sv, part, smax, a.mean, a.s, a.kconst, a.H,
                        a.N, a.N_pad, g.R2, g.C1, a.k_sb, a.k_sh, a.k_sr, a.smooth_k, a.fold);
   else
-    hipLaunchKernelGGL((k_quant_kernel<T, false>), dim3((unsigned)g.C2, (unsigned)BH), dim3(PT), 0,
+    hipLaunchKernelGGL((k_quant_kernel<T, false, D>), dim3((unsigned)g.C2, (unsigned)BH), dim3(PT), 0,
                        stream, (const T*)a.k, (u8*)a.k8, a.sk, a.sv, part, smax, a.mean, a.s, a.kconst, a.H,
                        a.N, a.N_pad, g.R2, g.C1, a.k_sb, a.k_sh, a.k_sr, a.smooth_k, a.fold);
   return hipGetLastError();
 }
 
 hipError_t launch_prologue(const PrologueArgs& a, hipStream_t stream) {
-  return a.dtype == 1 ? launch_prologue_t<bf16>(a, stream) : launch_prologue_t<f16>(a, stream);
+  if (a.D == 64)
+    return a.dtype == 1 ? launch_prologue_t<bf16, 64>(a, stream)
+                        : launch_prologue_t<f16, 64>(a, stream);
+  return a.dtype == 1 ? launch_prologue_t<bf16, 128>(a, stream)
+                      : launch_prologue_t<f16, 128>(a, stream);
 }
 
 }  // namespace sage

@@ -27,7 +27,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int HD = 128;          // head_dim served by every kernel
+constexpr int HD = 128;          // the largest head_dim served (64 is the other)
 constexpr int NPAD = 64;         // N_pad granule
 constexpr float P_SCALE = 448.0f;
 constexpr float I8_MAX = 127.0f;
@@ -79,12 +79,13 @@ __device__ __forceinline__ uint32_t i8x4(float a, float b, float c, float d) {
   return i8_rne(a) | (i8_rne(b) << 8) | (i8_rne(c) << 16) | (i8_rne(d) << 24);
 }
 
-// Max over the 16 lanes of an aligned 16-lane group (lanes 16g .. 16g+15).
-__device__ __forceinline__ float max16(float x) {
+// Max over the G lanes of an aligned G-lane group (G = 8 or 16: lanes Gg .. Gg+G-1).
+template <int G = 16>
+__device__ __forceinline__ float maxg(float x) {
   x = fmaxf(x, __shfl_xor(x, 1, 64));
   x = fmaxf(x, __shfl_xor(x, 2, 64));
   x = fmaxf(x, __shfl_xor(x, 4, 64));
-  x = fmaxf(x, __shfl_xor(x, 8, 64));
+  if (G == 16) x = fmaxf(x, __shfl_xor(x, 8, 64));
   return x;
 }
 

@@ -6,7 +6,8 @@
 
 namespace sage {
 
-// Geometry of the two-launch prologue for BH planes of N rows (N_pad = ceil(N/64)*64).
+// Geometry of the two-launch prologue for BH planes of N rows (N_pad = ceil(N/64)*64). The
+// workspace is sized for head_dim 128, which covers 64.
 //   stats pass: grid (C1, BH), each block owns R1 consecutive rows of one plane;
 //   quant pass: grid (ceil(N_pad/R2), BH), each block owns R2 rows.
 // Blocks are sized so that small calls still spread over the chip and large calls keep the
@@ -14,7 +15,7 @@ namespace sage {
 struct PrologueGeom {
   int64_t R1, C1, R2, C2;
 };
-PrologueGeom prologue_geom(int64_t BH, int64_t N_pad);
+PrologueGeom prologue_geom(int64_t BH, int64_t N_pad, int64_t step = 128);
 size_t prologue_workspace_bytes(int64_t BH, int64_t N_pad);
 
 struct PrologueArgs {
@@ -24,6 +25,7 @@ struct PrologueArgs {
   const void* v;
   int64_t v_sb, v_sh, v_sr;
   int64_t B, H, N, N_pad;
+  int64_t D;       // head_dim: 64 or 128
   void* k8;
   float* sk;
   void* v8t;
@@ -47,6 +49,7 @@ struct AttnArgs {
   void* o;
   int64_t o_sb, o_sh, o_sr;
   int64_t B, H, N;          // query side: B*H planes of N rows
+  int64_t D;                // head_dim: 64 or 128 (the 256-query kernel serves 128 only)
   int64_t H_kv, N_kv, N_kv_pad;   // key/value side: B*H_kv planes of N_kv rows (H % H_kv == 0)
   float sm_scale;
   float* lse;              // optional (B*H, N) fp32 row logsumexp
@@ -62,6 +65,7 @@ struct QuantQArgs {
   const void* q;
   int64_t q_sb, q_sh, q_sr;
   int64_t B, H, N;
+  int64_t D;       // head_dim: 64 or 128
   float sm_scale;
   void* q8;
   float* sq;

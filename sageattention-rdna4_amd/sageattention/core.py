@@ -7,9 +7,9 @@ sk1_backend=None, sk1_int8=None, sk1_bf16=None, **kwargs)`, with `smooth_k` (def
 
 There is exactly one backend here, the gfx950 library. A call outside its envelope raises a clear
 error instead of silently falling back (the reference falls back to its PR #368 path): `attn_mask`
-raises `NotImplementedError` as in `core.py:1156-1161`; any other miss (head_dim != 128, H not a
-multiple of H_kv, causal with q_len != kv_len, other dtypes) raises `ValueError` naming the
-reason. `return_lse=True` returns `(out, lse)` with lse (B, H, N) fp32 as the reference's
+raises `NotImplementedError` as in `core.py:1156-1161`; any other miss (head_dim not 64 or 128,
+H not a multiple of H_kv, causal with q_len != kv_len, other dtypes) raises `ValueError` naming
+the reason. `return_lse=True` returns `(out, lse)` with lse (B, H, N) fp32 as the reference's
 `core.py:1081-1095` defines it; grouped K/V heads and a key length of their own are served as the
 upstream API serves them (`core.py:824-829`); `smooth_v=True` subtracts V's sequence mean before
 quantizing V and adds it back to the output (`core.py:395-421`; in the SK1 scheme the reference's
@@ -27,10 +27,10 @@ def sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=None, retur
              sk1_backend=None, sk1_int8=None, sk1_bf16=None, **kwargs):
     """Quantized self-attention: int8 (fp16 inputs) or fp8 (bf16 inputs) Q.K, fp8 P.V.
 
-    q: (B, H, N, 128) for `tensor_layout="HND"` or (B, N, H, 128) for "NHD"; k, v likewise with
-    H_kv heads (H a multiple of H_kv: query head h reads K/V head h // (H // H_kv)) and N_kv rows
-    (N_kv == N when causal); fp16 or bf16, on a gfx950 device. Returns the output in q's layout
-    and dtype; with `return_lse=True`, the pair `(out, lse)`, lse (B, H, N) fp32: the natural-log
+    q: (B, H, N, D) for `tensor_layout="HND"` or (B, N, H, D) for "NHD", D = 64 or 128; k, v
+    likewise with H_kv heads (H a multiple of H_kv: query head h reads K/V head h // (H // H_kv))
+    and N_kv rows (N_kv == N when causal); fp16 or bf16, on a gfx950 device. Returns the output in
+    q's layout and dtype; with `return_lse=True`, the pair `(out, lse)`, lse (B, H, N) fp32: the natural-log
     logsumexp of each row of Q.K^T * sm_scale.
     kwargs: `smooth_k` (default True) subtracts the sequence mean of K before quantizing it;
     `smooth_v` (default False) subtracts V's and adds it back to the output.

@@ -26,11 +26,11 @@ from .sk1_loader import STRIDED_REFUSALS, SageLib, strided_view_reason  # noqa: 
 SUPPORTED_ARCHS = ("gfx950",)
 
 #: What this build serves. `layout` HND or NHD; `contiguous` = any view `strided_view_reason`
-#: accepts (contiguous HND, physically-NHD, fused-QKV splits); head_dim 128 only.
+#: accepts (contiguous HND, physically-NHD, fused-QKV splits); head_dim 64 or 128.
 ENVELOPE = dict(
     layout=("HND", "NHD"),
     dtype=("fp16", "bf16"),
-    head_dim=(128,),
+    head_dim=(64, 128),
     contiguous="any view strided_view_reason accepts",
     causal=(0, 1),
     smooth_k=(False, True),
@@ -97,7 +97,9 @@ def _envelope_ok(q, k, v, tensor_layout, is_causal, sm_scale, return_lse, smooth
         r = strided_view_reason(t, nm)
         if r is not None:
             return r
-    if q.size(3) != 128 or k.size(3) != q.size(3) or v.size(3) != q.size(3):
+    # head_dim 64 or 128, the three tensors agreeing (the reference's rule, `__init__.py:962-965`;
+    # its D=64 object is never routed, `:208-229`; here the 128-query main loop serves it)
+    if q.size(3) not in (64, 128) or k.size(3) != q.size(3) or v.size(3) != q.size(3):
         return "head_dim"
     if q.size(0) != k.size(0) or q.size(0) != v.size(0):
         return "batch"
@@ -167,7 +169,8 @@ def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=
     h // (H // H_kv); N may differ from N_kv when not causal. `smooth_v` subtracts V's sequence
     mean before quantizing V and adds it back to the output (exact, since each row's weights sum
     to 1; the reference's `quant_triton.py:668-678`).
-    `kernel` picks the main-loop kernel (0: by size, 1: 128 queries per block, 2: 256).
+    `kernel` picks the main-loop kernel (0: by size, 1: 128 queries per block, 2: 256, head_dim 128
+    only).
     With `return_lse`, returns `(out, lse)`: lse (B, H, N) fp32, each row's natural-log
     logsumexp of its scores times sm_scale (with smooth_k, corrected by sm_scale * q . mean_k, as
     the reference's `core.py:1437-1439`).

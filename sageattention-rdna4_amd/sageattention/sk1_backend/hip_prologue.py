@@ -7,7 +7,8 @@ vocabulary `REFUSALS`, `check`, `quant_kv` (returns `(k8, sk, v8t, sv)` freshly 
 * the mean, the K/V quantization and the per-(b,h) V-scale fold run as two launches of one library
   call; `quant_kv(..., fold=True)` also returns `S` and leaves `SV' = SV/S` in `sv` (the reference
   runs `fold_v_scale`, three torch ops, afterwards: `sk1_backend/__init__.py:561-579`);
-* head_dim is 128 only (the reference's D=64 prologue feeds no served kernel);
+* head_dim is 64 or 128, as the reference's (its D=64 prologue feeds no served kernel there;
+  here the 128-query main loop serves D=64);
 * `floor` is fixed at the reference's 1e-12.
 """
 import collections
@@ -16,7 +17,7 @@ import torch
 
 from .sk1_loader import SageLib, strided_view_reason
 
-HD = 128
+HEAD_DIMS = (64, 128)
 BN = 64
 FLOOR = 1e-12
 
@@ -73,7 +74,7 @@ class HipPrologue:
                 return "bf16_int8"
         elif k.dtype != torch.float16:
             return "dtype"
-        if int(k.shape[3]) != HD:
+        if int(k.shape[3]) not in HEAD_DIMS:
             return "head_dim"
         if k.device != v.device:
             return "device"
@@ -92,10 +93,11 @@ class HipPrologue:
 
     def quant_kv(self, k, v, n_pad=None, smooth_k=False, int8=True, floor=FLOOR, fold=False,
                  mean_out=False):
-        """`(k8, sk, v8t, sv)` for logical (B, H, N, 128) fp16/bf16 `k`/`v`, or `None` if refused.
+        """`(k8, sk, v8t, sv)` for logical (B, H, N, D) fp16/bf16 `k`/`v` (D = 64 or 128), or
+        `None` if refused.
 
         With `fold=True` the tuple gains `S` (B*H,) and `sv` holds `SV' = SV / S`. With
-        `mean_out=True` (and smooth_k) the tuple also gains the mean (B*H, 128). Never raises: a
+        `mean_out=True` (and smooth_k) the tuple also gains the mean (B*H, D). Never raises: a
         refusal or a launch error returns `None` and is counted in `refusal_reasons`.
         """
         if k.dim() != 4 or v.dim() != 4:
@@ -133,11 +135,11 @@ class HipPrologue:
         return res
 
     def kseq_mean(self, k):
-        """The smooth_k sequence mean (B, H, 128) fp32, or `None` if refused."""
+        """The smooth_k sequence mean (B, H, D) fp32, or `None` if refused."""
         if k.dim() != 4 or not k.is_cuda or k.dtype not in (torch.float16, torch.bfloat16):
             return self._refuse("mean_dtype")
         B, H, N, D = (int(x) for x in k.shape)
-        if D != HD:
+        if D not in HEAD_DIMS:
             return self._refuse("mean_head_dim")
         r = strided_view_reason(k, "k")
         if r is not None:

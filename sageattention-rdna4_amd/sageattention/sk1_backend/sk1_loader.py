@@ -104,17 +104,18 @@ class SageLib:
         L.sage_kv_prologue_workspace_bytes.restype = ctypes.c_size_t
         L.sage_kv_prologue_workspace_bytes.argtypes = [i64, i64]
         L.sage_kv_prologue.restype = i32
-        L.sage_kv_prologue.argtypes = ([i32] * 5 + [vp, i64, i64, i64] * 2 + [i64] * 4
+        L.sage_kv_prologue.argtypes = ([i32] * 5 + [vp, i64, i64, i64] * 2 + [i64] * 5
                                        + [vp] * 9 + [ctypes.c_size_t, vp])
         L.sage_attn_fwd.restype = i32
         L.sage_attn_fwd.argtypes = ([i32] * 3 + [vp, i64, i64, i64] + [vp] * 4
                                     + [vp, i64, i64, i64] + [i64] * 4 + [f32, vp])
         L.sage_attn_fwd_ex.restype = i32
         L.sage_attn_fwd_ex.argtypes = ([i32] * 3 + [vp, i64, i64, i64] + [vp] * 4
-                                       + [vp, i64, i64, i64] + [i64] * 6
+                                       + [vp, i64, i64, i64] + [i64] * 7
                                        + [f32, i32, vp, vp, vp, vp])
         L.sage_quant_q.restype = i32
-        L.sage_quant_q.argtypes = [i32, i32, vp, i64, i64, i64, i64, i64, i64, f32, vp, vp, vp, vp]
+        L.sage_quant_q.argtypes = [i32, i32, vp, i64, i64, i64, i64, i64, i64, i64, f32, vp, vp,
+                                   vp, vp]
         L.sage_mfma_layout_probe.restype = i32
         L.sage_mfma_layout_probe.argtypes = [vp] * 7
         self.version = int(L.sage_version())
@@ -133,15 +134,16 @@ class SageLib:
     # ------------------------------------------------------------------ entry points
     def kv_prologue(self, k, v, k8, sk, v8t, sv, s, mean, workspace, *, k_int8, smooth_k, fold,
                     n_pad, kconst=None, smooth_v=False, vmean=None):
-        """K/V prologue on logical (B, H, N, D) views `k`, `v` (see `sage_kv_prologue`).
+        """K/V prologue on logical (B, H, N, D) views `k`, `v`, D = 64 or 128 (see
+        `sage_kv_prologue`).
         `kconst` (optional) receives the main loop's per-key constants, (B*H, N_pad/64, 3, 64);
         with `smooth_v`, `vmean` ((B*H, 128) fp32) receives V's sequence mean."""
-        B, H, N, _ = (int(x) for x in k.shape)
+        B, H, N, D = (int(x) for x in k.shape)
         rc = self.lib.sage_kv_prologue(
             _dtype_code(k.dtype), int(bool(k_int8)), int(bool(smooth_k)), int(bool(smooth_v)),
             int(bool(fold)), _ptr(k), k.stride(0), k.stride(1), k.stride(2),
             _ptr(v), v.stride(0), v.stride(1), v.stride(2),
-            B, H, N, int(n_pad), _ptr(k8), _ptr(sk), _ptr(v8t), _ptr(sv), _ptr(mean),
+            B, H, N, int(n_pad), D, _ptr(k8), _ptr(sk), _ptr(v8t), _ptr(sv), _ptr(mean),
             _ptr(vmean), _ptr(s), _ptr(kconst), _ptr(workspace),
             int(workspace.numel() * workspace.element_size()),
             ctypes.c_void_p(torch_stream(k.device)))
@@ -155,7 +157,7 @@ class SageLib:
         is then ceil(n_kv/64)*64). `lse` (optional, (B, H, N) fp32) receives each row's
         logsumexp; `kmean` ((B*H_kv, 128) fp32) adds its smooth_k correction; `vmean`
         ((B*H_kv, 128) fp32, optional) is added to every output row (smooth_v)."""
-        B, H, N, _ = (int(x) for x in q.shape)
+        B, H, N, D = (int(x) for x in q.shape)
         bh_kv = int(k8.shape[0])
         if bh_kv % B:
             raise ValueError("sage_attn_fwd: k8 holds %d planes, not a multiple of B=%d" % (bh_kv, B))
@@ -165,7 +167,7 @@ class SageLib:
             _ptr(q), q.stride(0), q.stride(1), q.stride(2),
             _ptr(k8), _ptr(kconst), _ptr(v8t), _ptr(s),
             _ptr(o), o.stride(0), o.stride(1), o.stride(2),
-            B, H, N, bh_kv // B, n_kv, int(n_pad), ctypes.c_float(float(sm_scale)), int(kernel),
+            B, H, N, bh_kv // B, n_kv, int(n_pad), D, ctypes.c_float(float(sm_scale)), int(kernel),
             _ptr(lse), _ptr(kmean), _ptr(vmean), ctypes.c_void_p(torch_stream(q.device)))
         self._check(rc, "sage_attn_fwd")
 
@@ -179,7 +181,7 @@ class SageLib:
         cq = torch.empty(B * H, N, device=dev, dtype=torch.float32)
         rc = self.lib.sage_quant_q(
             _dtype_code(q.dtype), int(bool(qk_int8)), _ptr(q), q.stride(0), q.stride(1),
-            q.stride(2), B, H, N, ctypes.c_float(float(sm_scale)), _ptr(q8), _ptr(sq), _ptr(cq),
+            q.stride(2), B, H, N, D, ctypes.c_float(float(sm_scale)), _ptr(q8), _ptr(sq), _ptr(cq),
             ctypes.c_void_p(torch_stream(dev)))
         self._check(rc, "sage_quant_q")
         return q8, sq, cq

@@ -28,7 +28,7 @@ from sage_testutil import make_qkv  # noqa: E402
 
 CASES = {
     # name: (dtype, B, H, N, causal, smooth_k, layout, std, k_offset, outliers, seed
-    #        [, H_kv, N_kv[, smooth_v, v_offset]])
+    #        [, H_kv, N_kv[, smooth_v, v_offset[, head_dim]]]])
     "fp16_n77_causal": (torch.float16, 1, 1, 77, True, True, "HND", 1.0, 2.0, 0.03, 11),
     "fp16_n1_noncausal": (torch.float16, 1, 2, 1, False, True, "HND", 1.0, 2.0, 0.0, 12),
     "fp16_n70_nhd_nosmooth": (torch.float16, 2, 1, 70, False, False, "NHD", 1.0, 0.0, 0.0, 13),
@@ -43,6 +43,11 @@ CASES = {
                                  2, 100, True, 4.0),
     "bf16_smoothv_gqa_n80_kv150": (torch.bfloat16, 1, 4, 80, False, False, "HND", 1.0, 0.0, 0.0,
                                    18, 2, 150, True, 3.0),
+    # head_dim 64
+    "fp16_d64_n90_causal": (torch.float16, 1, 2, 90, True, True, "HND", 1.0, 2.0, 0.03, 19,
+                            2, 90, False, 0.0, 64),
+    "bf16_d64_gqa_nhd_n50_kv77_smoothv": (torch.bfloat16, 1, 4, 50, False, True, "NHD", 1.0, 1.5,
+                                          0.0, 20, 2, 77, True, 2.0, 64),
 }
 
 
@@ -71,15 +76,16 @@ def make(name):
     dtype, B, H, N, causal, smooth_k, layout, std, off, outl, seed = CASES[name][:11]
     H_kv, N_kv = CASES[name][11:13] or (H, N)
     smooth_v, v_off = CASES[name][13:15] or (False, 0.0)
+    D = CASES[name][15] if len(CASES[name]) > 15 else 128
     q, k, v = make_qkv(B, H, N, seed=seed, dtype=dtype, layout=layout, std=std, k_offset_std=off,
-                       outlier_frac=outl, h_kv=H_kv, n_kv=N_kv, v_offset_std=v_off)
+                       outlier_frac=outl, h_kv=H_kv, n_kv=N_kv, v_offset_std=v_off, d=D)
     q, k, v = corner_rows(q, k, v, layout)
     r = oracle.emulate_sageattn(q, k, v, tensor_layout=layout, is_causal=causal, smooth_k=smooth_k,
                                 smooth_v=smooth_v)
     arr = dict(
-        # B, H, N, causal, smooth_k, NHD, bf16, H_kv, N_kv, smooth_v
+        # B, H, N, causal, smooth_k, NHD, bf16, H_kv, N_kv, smooth_v, head_dim
         meta=np.array([B, H, N, int(causal), int(smooth_k), int(layout == "NHD"),
-                       int(dtype == torch.bfloat16), H_kv, N_kv, int(smooth_v)], dtype=np.int64),
+                       int(dtype == torch.bfloat16), H_kv, N_kv, int(smooth_v), D], dtype=np.int64),
         sm_scale=np.array([r["sm_scale"]], dtype=np.float32),
         q=bits(q), k=bits(k), v=bits(v),
         k8=bits(r["k8"]) if r["k8"].dtype != torch.int8 else r["k8"].numpy(),

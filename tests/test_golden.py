@@ -26,10 +26,10 @@ def _load(path):
 
 
 def _inputs(g):
-    B, H, N, causal, smooth_k, nhd, bf16, H_kv, N_kv, smooth_v = (int(x) for x in g["meta"])
+    B, H, N, causal, smooth_k, nhd, bf16, H_kv, N_kv, smooth_v, D = (int(x) for x in g["meta"])
     dtype = torch.bfloat16 if bf16 else torch.float16
-    shape = (B, N, H, 128) if nhd else (B, H, N, 128)
-    kv_shape = (B, N_kv, H_kv, 128) if nhd else (B, H_kv, N_kv, 128)
+    shape = (B, N, H, D) if nhd else (B, H, N, D)
+    kv_shape = (B, N_kv, H_kv, D) if nhd else (B, H_kv, N_kv, D)
     q = torch.from_numpy(g["q"].astype(np.int16)).view(dtype).reshape(shape)
     k, v = (torch.from_numpy(g[n].astype(np.int16)).view(dtype).reshape(kv_shape) for n in "kv")
     return q, k, v, dict(causal=bool(causal), smooth_k=bool(smooth_k), smooth_v=bool(smooth_v),

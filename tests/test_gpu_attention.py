@@ -201,11 +201,11 @@ def test_fused_qkv_views_served_bitwise(dtype, smooth_k):
     assert torch.equal(out, ref)
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_head_dim_64_is_refused(dtype):
-    # The reference falls back to its PR #368 kernels for D=64; this build has one backend and
-    # refuses with a clear error.
-    q, k, v = (t.cuda() for t in make_qkv(1, 4, 512, seed=7, dtype=dtype, d=64))
+@pytest.mark.parametrize("d", [32, 96, 256])
+def test_other_head_dims_are_refused(d):
+    # head_dim 64 and 128 are served; the reference falls back to its PR #368 kernels for others,
+    # this build has one backend and refuses with a clear error.
+    q, k, v = (t.cuda() for t in make_qkv(1, 4, 512, seed=7, dtype=torch.float16, d=d))
     with pytest.raises(ValueError, match="head_dim"):
         _sageattn()(q, k, v, tensor_layout="HND")
 
@@ -449,3 +449,72 @@ def test_smooth_v_both_kernels_and_gqa_bitwise(causal):
     torch.cuda.synchronize()
     assert torch.equal(o1, o2) and torch.equal(o1, o_rep)
     assert torch.equal(l1, l_plain)          # the scores, and so the logsumexp, do not involve V
+
+
+# ---------------------------------------------------------------------------------------------
+# head_dim 64: the 128-query kernel with two Q.K MFMAs per 32-key tile (int8) or one (fp8), two
+# 32-channel output tiles and 4 KB K and V^T tiles. The reference builds a D=64 object but never
+# routes it (`sageattention/sk1_backend/__init__.py:208-229`); here it is served, held to the
+# same bars as D=128.
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("N", [1, 63, 65, 129, 300, 1000, 4096])
+def test_d64_matches_emulation(N, causal, dtype):
+    q, k, v = make_qkv(1, 3, N, seed=N + 5, dtype=dtype, k_offset_std=2.0, outlier_frac=0.01,
+                       d=64)
+    print("N", N, causal, dtype, flush=True)
+    _check_vs_oracle(q, k, v, causal=causal)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_d64_close_to_exact_attention(causal, dtype):
+    q, k, v = make_qkv(2, 4, 777, seed=3, dtype=dtype, d=64)
+    out = _sageattn()(q.cuda(), k.cuda(), v.cuda(), is_causal=causal).cpu()
+    err = rel_rms(out, oracle.exact_attention(q, k, v, is_causal=causal))
+    print("rel_rms vs exact %.4f" % err)
+    assert err < MAX_REL_RMS
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_d64_nhd_equals_hnd_bitwise(causal):
+    q, k, v = make_qkv(2, 3, 333, seed=8, dtype=torch.float16, layout="NHD", d=64,
+                       k_offset_std=1.0)
+    o_nhd = _sageattn()(q.cuda(), k.cuda(), v.cuda(), tensor_layout="NHD", is_causal=causal).cpu()
+    hnd = [t.transpose(1, 2).contiguous() for t in (q, k, v)]
+    o_hnd = _sageattn()(*(t.cuda() for t in hnd), is_causal=causal).cpu()
+    assert torch.equal(o_nhd.transpose(1, 2), o_hnd)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(1, 8, 2, 500, 500, True), (2, 4, 1, 70, 1000, False),
+                                   (1, 6, 3, 1000, 77, False)],
+                         ids=lambda s: "H%dkv%dN%dNk%d%s" % (s[1], s[2], s[3], s[4],
+                                                              "c" if s[5] else ""))
+def test_d64_gqa_lse_smooth_v_match_emulation(shape, dtype):
+    B, H, H_kv, N, N_kv, causal = shape
+    q, k, v = make_qkv(B, H, N, seed=N + N_kv + 1, dtype=dtype, k_offset_std=2.0, h_kv=H_kv,
+                       n_kv=N_kv, v_offset_std=3.0, d=64)
+    for smooth_v in (False, True):
+        r = oracle.emulate_sageattn(q, k, v, is_causal=causal, smooth_v=smooth_v)
+        out, lse = _sageattn()(q.cuda(), k.cuda(), v.cuda(), is_causal=causal, return_lse=True,
+                               smooth_v=smooth_v)
+        torch.cuda.synchronize()
+        out, lse = out.cpu(), lse.cpu()
+        cs, rl = cosine(out, r["o"]), rel_l1(out, r["o"])
+        print(shape, dtype, smooth_v, "cos %.6f rel_l1 %.2e" % (cs, rl))
+        assert cs >= COS_MIN and rl <= REL_L1_MAX, (cs, rl)
+        _lse_close(lse, r, B, H, dtype == torch.bfloat16)
+
+
+def test_d64_refuses_the_256_query_kernel():
+    from sageattention.sk1_backend import sk1_forward
+    from sageattention.sk1_backend.sk1_loader import SageLib
+    q, k, v = (t.cuda() for t in make_qkv(1, 2, 100, seed=1, d=64))
+    with pytest.raises(ValueError, match="kernel"):
+        sk1_forward(SageLib.get(), q, k, v, kernel=2)
+    o0 = sk1_forward(SageLib.get(), q, k, v, kernel=0)
+    o1 = sk1_forward(SageLib.get(), q, k, v, kernel=1)
+    torch.cuda.synchronize()
+    assert torch.equal(o0, o1)

@@ -205,3 +205,59 @@ def test_fp8_convert_matches_torch_on_all_fp16_in_range():
     ref = vals.reshape(rows, HEAD_DIM).float().to(torch.float8_e4m3fn).t()
     assert (got["sv"][0, :rows] == 1.0).all()
     assert bytes_equal(got["v8t"][0, :, :rows].contiguous(), ref.contiguous())
+
+
+D64_CASES = [
+    # (dtype, k_int8, N, H, k_offset, outliers, std)
+    (torch.float16, True, 1, 2, 2.0, 0.0, 1.0),
+    (torch.float16, True, 65, 2, 2.0, 0.0, 1.0),
+    (torch.float16, True, 300, 3, 2.0, 0.01, 1.0),
+    (torch.float16, True, 4097, 2, 2.0, 0.001, 1.0),
+    (torch.float16, False, 300, 2, 2.0, 0.0, 1.0),
+    (torch.bfloat16, False, 129, 2, 2.0, 0.0, 1.5),
+    (torch.bfloat16, False, 2000, 3, 2.0, 0.001, 1.5),
+]
+
+
+@pytest.mark.parametrize("smooth_v", [False, True])
+@pytest.mark.parametrize("smooth_k", [True, False])
+@pytest.mark.parametrize("case", D64_CASES, ids=lambda c: "%s-%s-N%d" % (
+    str(c[0]).split(".")[-1], "i8" if c[1] else "f8", c[2]))
+def test_prologue_d64_bit_exact(case, smooth_k, smooth_v):
+    # head_dim 64: 8 column groups x 32 row groups, 256-row stats steps (blocks of a multiple of
+    # 256 rows), the same arithmetic; a V row far above 448 exercises the fold.
+    dtype, k_int8, N, H, off, outl, std = case
+    q, k, v = make_qkv(1, H, N, seed=N + 3 * H, dtype=dtype, std=std, k_offset_std=off,
+                       outlier_frac=outl, v_offset_std=2.0, d=64)
+    if N > 9:
+        v[0, 1, 9] = 5000.0
+    print("case", case, smooth_k, smooth_v, flush=True)
+    ref = _oracle_prologue(k, v, k_int8=k_int8, smooth_k=smooth_k, smooth_v=smooth_v)
+    got = _run_prologue(k.cuda(), v.cuda(), k_int8=k_int8, smooth_k=smooth_k, fold=True,
+                        smooth_v=smooth_v, with_kconst=True)
+    if smooth_k:
+        assert bytes_equal(got["mean"], ref["mean"]), mismatch_report(got["mean"], ref["mean"], "mean")
+    if smooth_v:
+        assert bytes_equal(got["vmean"], ref["vmean"]), mismatch_report(got["vmean"], ref["vmean"],
+                                                                        "vmean")
+    for name, rname in (("k8", "k8"), ("sk", "sk"), ("v8t", "v8t"), ("sv", "svp"), ("s", "s")):
+        assert bytes_equal(got[name], ref[rname]), mismatch_report(got[name], ref[rname], name)
+    n_pad = oracle.n_pad_for(N)
+    kc = got["kconst"].reshape(H, n_pad // 64, 3, 64)
+    assert bytes_equal(kc[:, :, 0].contiguous(), got["sk"].reshape(H, n_pad // 64, 64))
+    w = got["sv"].reshape(H, n_pad // 64, 64) * oracle.P_SCALE
+    assert bytes_equal(kc[:, :, 2].contiguous(), w)
+
+
+@pytest.mark.parametrize("dtype,qk_int8", [(torch.float16, True), (torch.float16, False),
+                                           (torch.bfloat16, False)])
+@pytest.mark.parametrize("N", [1, 33, 300])
+def test_quant_q_d64_bit_exact(dtype, qk_int8, N):
+    q, k, v = make_qkv(1, 3, N, seed=11 + N, dtype=dtype, std=1.5, d=64)
+    q[0, 1, : min(N, 5)] = 0.0
+    sm = 64 ** -0.5
+    q8, sq, cq = _lib().quant_q(q.cuda(), sm, qk_int8=qk_int8)
+    torch.cuda.synchronize()
+    r8, rsq, rcq = oracle.quant_q(q.reshape(3, N, 64), sm, int8=qk_int8)
+    assert bytes_equal(q8.cpu(), r8), mismatch_report(q8.cpu(), r8, "q8")
+    assert bytes_equal(sq.cpu(), rsq) and bytes_equal(cq.cpu(), rcq)

@@ -54,19 +54,19 @@ def test_library_host_calls_without_a_gpu():
     rc = L.lib.sage_attn_fwd(0, 1, 1, None, 8, 8, 8, None, None, None, None, None, 8, 8, 8,
                              1, 1, 0, 64, ctypes.c_float(0.1), None)
     assert rc == 1 and b"n_lt_1" in L.lib.sage_last_error()
-    rc = L.lib.sage_kv_prologue(1, 1, 1, 0, 1, None, 8, 8, 8, None, 8, 8, 8, 1, 1, 10, 64,
+    rc = L.lib.sage_kv_prologue(1, 1, 1, 0, 1, None, 8, 8, 8, None, 8, 8, 8, 1, 1, 10, 64, 128,
                                 *([None] * 9), 0, None)
     assert rc == 1 and b"bf16_int8" in L.lib.sage_last_error()
     rc = L.lib.sage_kv_prologue(0, 1, 1, 0, 1, ctypes.c_void_p(16), 8, 8, 4, ctypes.c_void_p(16),
-                                8, 8, 8, 1, 1, 10, 64, *([None] * 9), 0, None)
+                                8, 8, 8, 1, 1, 10, 64, 128, *([None] * 9), 0, None)
     assert rc == 1 and b"stride_align" in L.lib.sage_last_error()
     rc = L.lib.sage_attn_fwd(0, 1, 0, ctypes.c_void_p(16), 8, 8, 8, None, None, None, None,
                              ctypes.c_void_p(16), 8, 8, 8, 1, 1, 100, 96, ctypes.c_float(0.1), None)
     assert rc == 1 and b"n_pad" in L.lib.sage_last_error()
     p16 = ctypes.c_void_p(16)
-    def ex(causal=0, H=1, N=100, H_kv=1, N_kv=100, N_kv_pad=128, kernel=0, lse=None):
+    def ex(causal=0, H=1, N=100, H_kv=1, N_kv=100, N_kv_pad=128, kernel=0, lse=None, D=128):
         return L.lib.sage_attn_fwd_ex(0, 1, causal, p16, 12800, 12800, 128, p16, p16, p16, p16,
-                                      p16, 12800, 12800, 128, 1, H, N, H_kv, N_kv, N_kv_pad,
+                                      p16, 12800, 12800, 128, 1, H, N, H_kv, N_kv, N_kv_pad, D,
                                       ctypes.c_float(0.1), kernel, lse, None, None, None)
     assert ex(kernel=7) == 1 and b"kernel" in L.lib.sage_last_error()
     assert ex(lse=ctypes.c_void_p(18)) == 1
@@ -77,10 +77,16 @@ def test_library_host_calls_without_a_gpu():
     assert ex(causal=1, N_kv=99) == 1 and b"seq_len" in L.lib.sage_last_error()
     assert ex(N_kv=200, N_kv_pad=192) == 1 and b"n_pad" in L.lib.sage_last_error()
     assert ex(N_kv=0, N_kv_pad=64) == 1 and b"n_lt_1" in L.lib.sage_last_error()
+    # head_dim 64 or 128; 64 only on the 128-query kernel
+    assert ex(D=96) == 1 and b"head_dim" in L.lib.sage_last_error()
+    assert ex(D=64, kernel=2) == 1 and b"kernel" in L.lib.sage_last_error()
+    rc = L.lib.sage_quant_q(0, 1, p16, 12800, 12800, 128, 1, 1, 100, 32, ctypes.c_float(0.1),
+                            p16, p16, p16, None)
+    assert rc == 1 and b"head_dim" in L.lib.sage_last_error()
     # smooth_v needs somewhere to put V's mean
     rc = L.lib.sage_kv_prologue(0, 1, 1, 1, 1, p16, 12800, 12800, 128, p16, 12800, 12800, 128,
-                                1, 1, 100, 128, p16, p16, p16, p16, None, None, p16, None, p16,
-                                1 << 20, None)
+                                1, 1, 100, 128, 128, p16, p16, p16, p16, None, None, p16, None,
+                                p16, 1 << 20, None)
     assert rc == 1 and b"vmean" in L.lib.sage_last_error()
 
 

@@ -103,9 +103,10 @@ def _k_int8_exact(row, mu=None):
     return sk, k8
 
 
-def test_quant_k_int8_exact_small():
-    q, k, v = make_qkv(1, 2, 37, seed=3, k_offset_std=2.0, outlier_frac=0.05)
-    kr = k.reshape(2, 37, 128)
+@pytest.mark.parametrize("d", [128, 64])
+def test_quant_k_int8_exact_small(d):
+    q, k, v = make_qkv(1, 2, 37, seed=3, k_offset_std=2.0, outlier_frac=0.05, d=d)
+    kr = k.reshape(2, 37, d)
     mean = oracle.kseq_mean(kr)
     k8, sk = oracle.quant_k(kr, 64, mean=mean, int8=True)
     for bh in range(2):
@@ -152,11 +153,12 @@ def test_quant_k_fp8_and_v_exact_small():
     assert (sv[0, 20:] == 0).all() and (v8t[0, :, 20:].view(torch.uint8) == 0).all()
 
 
-def test_quant_q_exact_small():
+@pytest.mark.parametrize("d", [128, 64])
+def test_quant_q_exact_small(d):
     # Q uses a multiplication by the correctly rounded reciprocal (`sk1_t6i.hip:108`, `:115`).
-    q, k, v = make_qkv(1, 1, 24, seed=9, std=1.3)
-    qr = q.reshape(1, 24, 128)
-    sm = 128 ** -0.5
+    q, k, v = make_qkv(1, 1, 24, seed=9, std=1.3, d=d)
+    qr = q.reshape(1, 24, d)
+    sm = d ** -0.5
     for int8 in (True, False):
         q8, sq, cq = oracle.quant_q(qr, sm, int8=int8)
         top = 127 if int8 else 448
@@ -206,7 +208,7 @@ def _brute_force_row(q8r, cqr, k8, sk, v8t, svp, S, row, N, causal, int8, tile=6
     n_pad = k8.shape[0]
     qv = q8r.astype(np.float64)
     m, l = f32(-np.inf), f32(0)
-    acc = np.zeros(128, dtype=np.float32)
+    acc = np.zeros(v8t.shape[0], dtype=np.float32)
     for j0 in range(0, n_pad, tile):
         s = []
         for n in range(j0, j0 + tile):
@@ -231,10 +233,11 @@ def _brute_force_row(q8r, cqr, k8, sk, v8t, svp, S, row, N, causal, int8, tile=6
     return (acc * inv).astype(np.float32)
 
 
+@pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("N", [5, 64, 130])
-def test_attention_tiles_vs_brute_force(N, causal):
-    q, k, v = make_qkv(1, 1, N, seed=N, k_offset_std=1.0)
+def test_attention_tiles_vs_brute_force(N, causal, d):
+    q, k, v = make_qkv(1, 1, N, seed=N, k_offset_std=1.0, d=d)
     r = oracle.emulate_sageattn(q, k, v, is_causal=causal)
     k8 = r["k8"][0].numpy().astype(np.int32)
     v8t = r["v8t"][0].float().numpy()
@@ -345,11 +348,12 @@ def test_lse_close_to_exact_and_needs_the_correction():
         assert (r["lse"][0] - corr - ex[0]).abs().max().item() > 0.5
 
 
-def test_emulation_close_to_exact_attention():
+@pytest.mark.parametrize("d", [128, 64])
+def test_emulation_close_to_exact_attention(d):
     # The scheme's error against exact attention on N(0,1) inputs: the reference's bar is 0.08
     # relative RMS (`tests/test_sk1_backend.py:28-29`), observed 0.03-0.055.
     for dtype in (torch.float16, torch.bfloat16):
-        q, k, v = make_qkv(1, 4, 512, seed=1, dtype=dtype)
+        q, k, v = make_qkv(1, 4, 512, seed=1, dtype=dtype, d=d)
         for causal in (False, True):
             o = oracle.emulate_sageattn(q, k, v, is_causal=causal)["o"].double()
             ex = oracle.exact_attention(q, k, v, is_causal=causal)
