@@ -213,9 +213,9 @@ def main():
     lib = SageLib.get()
     call = lambda ev=None: sk1_forward(lib, qd, kd, vd, tensor_layout=layout, is_causal=causal,
                                        smooth_k=True, events=ev, kernel=args.kernel)
-    # the library's choice by size (sage_attn_fwd_ex): 256 queries per block from N = 16384 on,
+    # the library's choice by size (sage_attn_fwd_ex): 256 queries per block from N = 32768 on,
     # head_dim 128 only
-    q256 = args.kernel == 2 or (args.kernel == 0 and N >= 16384 and D == 128)
+    q256 = args.kernel == 2 or (args.kernel == 0 and N >= 32768 and D == 128)
     kname = "attn_fwd_pp_kernel" if q256 else "attn_fwd_kernel"
     for _ in range(args.warmup):
         call()

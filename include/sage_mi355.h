@@ -36,7 +36,7 @@ extern "C" {
 #define SAGE_BF16 1
 
 /* main-loop kernel choice of sage_attn_fwd_ex */
-#define SAGE_KERNEL_AUTO 0  /* by size: the 256-query ping-pong from N = 16384 on, else 128 */
+#define SAGE_KERNEL_AUTO 0  /* by size: the 256-query ping-pong from N = 32768 on, else 128 */
 #define SAGE_KERNEL_Q128 1  /* 128 queries per block of 4 waves */
 #define SAGE_KERNEL_Q256 2  /* 256 queries per block of 8 waves, two groups in ping-pong */
 

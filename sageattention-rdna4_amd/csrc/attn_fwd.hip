@@ -37,7 +37,7 @@
 namespace sage {
 
 template <typename T, bool QK_INT8, bool CAUSAL, int D>
-__global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(SAGE_ATTN_WAVES, SAGE_ATTN_WAVES))) void attn_fwd_kernel(
+__global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(attn_waves(D), attn_waves(D)))) void attn_fwd_kernel(
     const T* __restrict__ Q, const u8* __restrict__ K8, const float* __restrict__ KC,
     const u8* __restrict__ V8T, const float* __restrict__ Sfold,
     T* __restrict__ O, int64_t q_sb, int64_t q_sh, int64_t q_sr, int64_t o_sb, int64_t o_sh,

@@ -254,8 +254,8 @@ def test_q256_kernel_nhd_equals_hnd_bitwise():
 
 
 def test_auto_kernel_choice_serves_long_sequences():
-    # N = 16384 takes the 256-query kernel by default; it must equal the 128-query kernel there.
-    q, k, v = make_qkv(1, 1, 16384, seed=21, dtype=torch.float16, k_offset_std=2.0)
+    # N = 32768 takes the 256-query kernel by default; it must equal the 128-query kernel there.
+    q, k, v = make_qkv(1, 1, 32768, seed=21, dtype=torch.float16, k_offset_std=2.0)
     o_auto = _forward(q, k, v, causal=True, kernel=0)
     o128 = _forward(q, k, v, causal=True, kernel=1)
     assert torch.equal(o_auto, o128)
