@@ -518,3 +518,39 @@ def test_d64_refuses_the_256_query_kernel():
     o1 = sk1_forward(SageLib.get(), q, k, v, kernel=1)
     torch.cuda.synchronize()
     assert torch.equal(o0, o1)
+
+
+# ---------------------------------------------------------------------------------------------
+# HIP graphs: the library allocates nothing and issues no memset, so a whole call (prologue and
+# main loop, with torch's allocations from the graph's pool) can be captured and replayed. Each
+# replay runs on new inputs copied into the captured buffers, with eager calls in between, and
+# must give the eager call's bits.
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("opts", [dict(is_causal=True), dict(is_causal=False, return_lse=True,
+                                                             smooth_v=True)],
+                         ids=["causal", "lse_smooth_v"])
+def test_graph_capture_replays_match_eager(opts):
+    sage = _sageattn()
+    inputs = [make_qkv(1, 4, 1000, seed=40 + i, dtype=torch.float16, k_offset_std=2.0)
+              for i in range(4)]
+    q, k, v = (t.cuda() for t in inputs[0])
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        sage(q, k, v, **opts)                       # warm-up (library load) off the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = sage(q, k, v, **opts)
+    for i in range(1, 4):
+        for dst, src in zip((q, k, v), inputs[i]):
+            dst.copy_(src.cuda())
+        eager = sage(q.clone(), k.clone(), v.clone(), **opts)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        if opts.get("return_lse"):
+            assert torch.equal(captured[0], eager[0]) and torch.equal(captured[1], eager[1]), i
+        else:
+            assert torch.equal(captured, eager), i
