@@ -18,15 +18,19 @@
 //   operand. (Which K row occupies which MFMA row is free: the reduction is over d.)
 // * The softmax is the VALU bottleneck (the MFMA work per score is 256 MACs = 1/16 clock per CU;
 //   the VALU runs 64 lanes per clock per CU), so it is written for the fewest VALU instructions per
-//   score: the int8 accumulator is seeded with the bit pattern of 1.5 * 2^23, which makes its
-//   result the float 1.5*2^23 + (Q8.K8) exactly, so ONE fma with (SK, -RN(1.5*2^23*SK)) gives
-//   x = (Q8.K8)*SK (to within one integer unit of the dot product); the running max is kept in
-//   x units per query, so the exp2 argument c_q*x - c_q*m is ONE more fma. Per score: fma, max3/2,
-//   fma, exp2, add, mul, cvt_pk/2.
-// * K, V and the per-key constants of block j+1 are loaded into registers at the top of block j
-//   and written to the other half of the double-buffered LDS at its bottom: one barrier per block.
+//   score: x = fp32(Q8.K8) * SK, with SK a DPP row broadcast folded into the multiply (no LDS read
+//   per score); the running max is kept in x units per query, so the exp2 argument c_q*x - mc is
+//   one fma; p*RN(SV'*448) is another DPP-broadcast multiply. Per score: cvt (int8 only), mul,
+//   max3/2, fma, exp2, add, mul, cvt_pk/2.
+// * Staging: K, V^T and the per-key constants go global -> LDS directly (global_load_lds), two
+//   blocks ahead into three LDS buffers; the DMAs are written as asm so that the loop's own
+//   s_waitcnt retires exactly the requests the next block needs, then one barrier per block.
 //   K rows use an XOR swizzle of their 16-byte chunks, V^T rows another, so the MFMA operand reads
 //   are bank-conflict free.
+// * Head dimension D = 128 or 64 (a template parameter): D/32 int8 (D/64 e4m3) Q.K MFMAs per
+//   32-key tile, D/32 output tiles, D-byte K rows. Occupancy: 3 waves per SIMD at D = 128, 4 at 64.
+// * Grouped K/V heads and a key length of their own: a block of query plane bh reads K/V plane
+//   b*H_kv + h/(H/H_kv); keys are bounded and masked by N_kv, queries by N.
 // * Causal: blocks past the CTA's diagonal are never visited, a wave skips blocks past its own
 //   diagonal, and masks are applied only on diagonal blocks. The grid is a 1-D list of (plane,
 //   q-tile) pairs, remapped so that each XCD (workgroup id mod 8) runs a contiguous range of

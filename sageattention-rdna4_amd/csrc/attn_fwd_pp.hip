@@ -3,8 +3,9 @@
 //
 // Scheme, layouts and per-score arithmetic are those of attn_fwd.hip (the reference's
 // kernels/hip/sk1_t6i.hip:84-299 and sk1_t4a1s.hip): transposed scores S^T = K . Q^T so that a
-// lane holds one query, the int8 accumulator seeded with 1.5 * 2^23, the exact running max in x
-// units, P folded into e4m3 as the P.V operand. What differs is the schedule.
+// lane holds one query, per-key constants as DPP row broadcasts, the exact running max in x units,
+// P folded into e4m3 as the P.V operand. What differs is the schedule (and this kernel serves
+// head_dim 128 only: at 64 its 8 waves would each stage half a 1 KB request).
 //
 // Why: per 64-key block a wave spends ~4x longer on its softmax (VALU) than on its MFMAs, and
 // the two can only overlap across waves. With two independent waves per SIMD the two tend to hit
