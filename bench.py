@@ -163,6 +163,25 @@ def cpu_baseline(wl, q, k, v, budget_s=20.0):
                 sdpa_cpu_gops=ops / ts / 1e9, sdpa_cpu_s=ts, host_cpus=os.cpu_count())
 
 
+def sclk_mhz():
+    """The GPU's current shader clock in MHz, read from sysfs (`pp_dpm_sclk`, where the current
+    level carries a `*`): a plain file read, so no other program is started from this process.
+    None where it is unavailable. With several AMD cards it reports the first one that has it."""
+    import glob
+    import re
+    for path in sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk")):
+        try:
+            with open(path) as f:
+                for line in f:
+                    if "*" in line:
+                        m = re.search(r"(\d+)\s*Mhz", line, re.IGNORECASE)
+                        if m:
+                            return int(m.group(1))
+        except OSError:
+            continue
+    return None
+
+
 def copy_calibration(mib, reps):
     """A plain device-to-device copy of `mib` MiB, `reps` times: each launch reads and writes
     exactly mib MiB, which calibrates what the HBM counters report per algorithmic byte."""
@@ -182,7 +201,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # about a second of calls at the headline: the shader clock ramps up over the first calls
+    # (measured 1836 MHz before a 2-call warm-up's timed region, 2277 MHz after it)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="c3c", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
@@ -223,12 +244,16 @@ def main():
 
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     torch.cuda.synchronize()
+    clk0 = sclk_mhz()
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         call(evs[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    clk1 = sclk_mhz()
     ms_step = wall * 1e3 / args.steps
+    steps_ms = sorted(e[0].elapsed_time(e[2]) for e in evs)
     pro_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
     attn_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
     ev_ms = sum(e[0].elapsed_time(e[2]) for e in evs) / args.steps
@@ -271,6 +296,12 @@ def main():
         "prologue": {"ms": round(pro_ms, 4), "bytes": pbytes, "achieved_GBps": round(pro_gbps, 1),
                      "peak_GBps": HBM_PEAK_GBPS, "frac": round(pro_gbps / HBM_PEAK_GBPS, 4)},
         "cpu_baseline": cpu,
+        # per-step full-call times from the HIP events (the same steps as ms_per_step) and the
+        # shader clock before and after the timed region: box-to-box clock differences are the
+        # largest source of spread between runs
+        "step_ms": {"min": round(steps_ms[0], 4), "median": round(steps_ms[len(steps_ms) // 2], 4),
+                    "max": round(steps_ms[-1], 4)},
+        "sclk_mhz": {"before": clk0, "after": clk1},
     }
     print(json.dumps(res), flush=True)
     return 0

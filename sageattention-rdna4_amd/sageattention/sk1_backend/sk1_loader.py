@@ -73,6 +73,19 @@ def _ptr(t):
     return ctypes.c_void_p(0 if t is None else int(t.data_ptr()))
 
 
+def hip_runtime_images():
+    """The distinct HIP runtime files (`libamdhip64`) mapped into this process, or None where
+    /proc/self/maps cannot be read. One image means the library and torch share the runtime (and
+    so torch's stream handles are valid for the library's launches), which the reference records
+    as its `same_as_torch` check (`sageattention/sk1_backend/sk1_loader.py:218-251`)."""
+    try:
+        with open("/proc/self/maps") as f:
+            maps = f.read()
+    except OSError:
+        return None
+    return sorted({ln.split()[-1] for ln in maps.splitlines() if "libamdhip64" in ln})
+
+
 class SageLib:
     """The loaded library. `SageLib.get()` loads it once per process (under a lock) and raises
     `RuntimeError` when it is missing or does not load: there is no other backend to fall back to."""
@@ -119,6 +132,9 @@ class SageLib:
         L.sage_mfma_layout_probe.restype = i32
         L.sage_mfma_layout_probe.argtypes = [vp] * 7
         self.version = int(L.sage_version())
+        images = hip_runtime_images()
+        self.hip_runtime = images
+        self.same_as_torch = None if images is None else len(images) == 1
 
     # ------------------------------------------------------------------ helpers
     def _check(self, rc, what):

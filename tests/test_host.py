@@ -90,6 +90,17 @@ def test_library_host_calls_without_a_gpu():
     assert rc == 1 and b"vmean" in L.lib.sage_last_error()
 
 
+def test_library_shares_torch_hip_runtime():
+    # the library's libamdhip64 dependency resolves to the image torch already loaded, so torch's
+    # stream handles are valid for its launches
+    from sageattention.sk1_backend import sk1_loader
+    if not os.path.isfile(sk1_loader.LIB_PATH):
+        pytest.skip("library not built")
+    L = sk1_loader.SageLib.get()
+    assert L.hip_runtime and len(L.hip_runtime) == 1, L.hip_runtime
+    assert L.same_as_torch is True
+
+
 def test_strided_view_reason_rule():
     from sageattention.sk1_backend.sk1_loader import strided_view_reason as r
     t = torch.empty(2, 4, 100, 128, dtype=torch.float16)
