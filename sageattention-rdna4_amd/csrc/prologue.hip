@@ -37,18 +37,24 @@ struct Geo {
   static constexpr int CG = D / 8, RG = PT / CG, STEP = 8 * RG, VTS = STEP + 16;
 };
 
+// Both grids are sized to one round of resident blocks on MI355X (256 CUs; a block is 4 waves, one
+// per SIMD): the stats pass fits 3 blocks per CU (at most 168 VGPRs; its 16 row loads of 16 bytes
+// per lane keep ~190 KB in flight per CU), the quant pass 8 (at most 64 VGPRs). A partly filled second round costs a streaming pass as much as a full one. Each plane gets
+// c = slots / BH blocks (at least 1) of equal row counts; a stats block's rows are a whole number
+// of its steps (128 rows for head_dim 128, 256 for 64), so no step reaches into the next block's
+// rows. A larger step only lowers C1, so the head_dim-128 geometry bounds the workspace for both.
+constexpr int64_t MI355_CUS = 256;
+constexpr int64_t STATS_BLOCKS_PER_CU = 3;
+constexpr int64_t QUANT_BLOCKS_PER_CU = 8;
+
 PrologueGeom prologue_geom(int64_t BH, int64_t N_pad, int64_t step) {
-  auto clampr = [](int64_t x, int64_t lo, int64_t hi) { return x < lo ? lo : (x > hi ? hi : x); };
-  auto up128 = [](int64_t x) { return (x + 127) / 128 * 128; };
+  auto cdiv = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
+  auto blocks_per_plane = [&](int64_t slots) { return BH < slots ? slots / BH : (int64_t)1; };
   PrologueGeom g;
-  // Aim for ~1024 stats blocks and ~2048 quant blocks on big calls. A stats block's rows are a
-  // whole number of its steps (128 rows for head_dim 128, 256 for 64), so no step reaches into
-  // the next block's rows; a larger step only lowers C1, so the head_dim-128 geometry bounds the
-  // workspace for both.
-  g.R1 = clampr((((N_pad * BH + 1023) / 1024) + step - 1) / step * step, step, 2048);
-  g.C1 = (N_pad + g.R1 - 1) / g.R1;
-  g.R2 = clampr(up128((N_pad * BH + 2047) / 2048), 128, 1024);
-  g.C2 = (N_pad + g.R2 - 1) / g.R2;
+  g.R1 = cdiv(cdiv(N_pad, blocks_per_plane(MI355_CUS * STATS_BLOCKS_PER_CU)), step) * step;
+  g.C1 = cdiv(N_pad, g.R1);
+  g.R2 = cdiv(cdiv(N_pad, blocks_per_plane(MI355_CUS * QUANT_BLOCKS_PER_CU)), 64) * 64;
+  g.C2 = cdiv(N_pad, g.R2);
   return g;
 }
 
@@ -78,7 +84,7 @@ size_t prologue_workspace_bytes(int64_t BH, int64_t N_pad) {
 enum VMode { V_QUANT = 0, V_SUMS = 1, V_CENTERED = 2 };
 
 template <typename T, int VMODE, int D>
-__global__ __launch_bounds__(PT) void kv_stats_kernel(
+__global__ __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(STATS_BLOCKS_PER_CU))) void kv_stats_kernel(
     const T* __restrict__ K, const T* __restrict__ V, u8* __restrict__ V8T, float* __restrict__ SV,
     double* __restrict__ part, double* __restrict__ vpart, float* __restrict__ VMEAN,
     float* __restrict__ smax, int64_t H, int64_t N, int64_t N_pad, int64_t R1, int64_t C1,
@@ -168,12 +174,15 @@ __global__ __launch_bounds__(PT) void kv_stats_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) vmax = fmaxf(vmax, fabsf(f[e]));
       vmax = maxg<G::CG>(vmax);
-      const float sv = fmaxf(__fdiv_rn(vmax, P_SCALE), SCALE_FLOOR);
+      // sv = max(RN(vmax / 448), 1e-12); the row's quotients RN(v / sv) come from one correctly
+      // rounded reciprocal of sv (div_by: bit-identical to a division per element)
+      const float sv = fmaxf(div_by(vmax, P_SCALE, RCP_P_SCALE), SCALE_FLOOR);
+      const float rsv = __fdiv_rn(1.0f, sv);
       if (cg == 0 && n < N_pad) SV[bh * N_pad + n] = live ? sv : 0.0f;
       if (live) sv_max = fmaxf(sv_max, sv);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const uint32_t byte = fp8x2(fminf(__fdiv_rn(f[e], sv), P_SCALE), 0.0f) & 0xffu;
+        const uint32_t byte = fp8x2(fminf(div_by(f[e], sv, rsv), P_SCALE), 0.0f) & 0xffu;
         if (i < 4)
           col_lo[e] |= byte << (8 * i);
         else
@@ -246,7 +255,7 @@ __global__ __launch_bounds__(PT) void kv_stats_kernel(
 // Quant pass. grid (C2, BH), block 256. Thread (cg, rg) handles row base+rg+16i, columns 8cg..+7.
 // ---------------------------------------------------------------------------------------------
 template <typename T, bool KINT8, int D>
-__global__ __launch_bounds__(PT) void k_quant_kernel(
+__global__ __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(QUANT_BLOCKS_PER_CU))) void k_quant_kernel(
     const T* __restrict__ K, u8* __restrict__ K8, float* __restrict__ SK, float* __restrict__ SV,
     const double* __restrict__ part, const float* __restrict__ smax, float* __restrict__ MEAN,
     float* __restrict__ S_out, float* __restrict__ KC, int64_t H, int64_t N, int64_t N_pad,
@@ -312,18 +321,21 @@ __global__ __launch_bounds__(PT) void k_quant_kernel(
         kmax = fmaxf(kmax, fabsf(kc[e]));
       }
       kmax = maxg<G::CG>(kmax);
-      const float sk = fmaxf(__fdiv_rn(kmax, KINT8 ? I8_MAX : P_SCALE), SCALE_FLOOR);
+      // sk = max(RN(kmax / 127 or 448), 1e-12); quotients RN(kc / sk) through one reciprocal
+      const float sk = fmaxf(KINT8 ? div_by(kmax, I8_MAX, RCP_I8_MAX)
+                                   : div_by(kmax, P_SCALE, RCP_P_SCALE), SCALE_FLOOR);
+      const float rsk = __fdiv_rn(1.0f, sk);
       if (n < r_end) {
         u32x2 word;
         if (KINT8) {
           float x[8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = __fdiv_rn(kc[e], sk);
+          for (int e = 0; e < 8; ++e) x[e] = div_by(kc[e], sk, rsk);
           word = (u32x2){i8x4(x[0], x[1], x[2], x[3]), i8x4(x[4], x[5], x[6], x[7])};
         } else {
           float x[8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = fminf(__fdiv_rn(kc[e], sk), P_SCALE);
+          for (int e = 0; e < 8; ++e) x[e] = fminf(div_by(kc[e], sk, rsk), P_SCALE);
           word = (u32x2){fp8x4(x[0], x[1], x[2], x[3]), fp8x4(x[4], x[5], x[6], x[7])};
         }
         *(u32x2*)(K8 + (bh * N_pad + n) * D + 8 * cg) = word;

@@ -81,13 +81,34 @@ __device__ __forceinline__ uint32_t i8x4(float a, float b, float c, float d) {
   return i8_rne(a) | (i8_rne(b) << 8) | (i8_rne(c) << 16) | (i8_rne(d) << 24);
 }
 
-// Max over the G lanes of an aligned G-lane group (G = 8 or 16: lanes Gg .. Gg+G-1).
+// RN(x / s) from y = RN(1 / s), in three operations instead of a full division: q = RN(x*y) is
+// within an ulp of x/s, e = RN(q*s - x) is then exact (one fma), and RN(q - e*y) is the correctly
+// rounded quotient (Markstein's theorem for round-to-nearest with a correctly rounded reciprocal).
+// The bits equal __fdiv_rn(x, s) for normal quotients; signed zeros pass through (-0 / s = -0).
+// The quantizers call it with one reciprocal per row (or a constant divisor), so a row of D
+// quotients costs one full division.
+__device__ __forceinline__ float div_by(float x, float s, float y) {
+  const float q = x * y;
+  const float e = __builtin_fmaf(q, s, -x);
+  return __builtin_fmaf(-e, y, q);
+}
+constexpr float RCP_P_SCALE = 1.0f / 448.0f;   // RN(1/448)
+constexpr float RCP_I8_MAX = 1.0f / 127.0f;    // RN(1/127)
+
+// One DPP lane move within each 16-lane row (ctrl: quad_perm / row_mirror / row_half_mirror).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Max over the G lanes of an aligned G-lane group (G = 8 or 16: lanes Gg .. Gg+G-1), as DPP
+// moves folded into v_max_f32: xor 1 and xor 2 (quad_perm), then the mirrored lane of the
+// 8-lane half-row (the other quad) and of the 16-lane row (the other half).
 template <int G = 16>
 __device__ __forceinline__ float maxg(float x) {
-  x = fmaxf(x, __shfl_xor(x, 1, 64));
-  x = fmaxf(x, __shfl_xor(x, 2, 64));
-  x = fmaxf(x, __shfl_xor(x, 4, 64));
-  if (G == 16) x = fmaxf(x, __shfl_xor(x, 8, 64));
+  x = fmaxf(x, dpp_mov<0xB1>(x));    // quad_perm [1,0,3,2]
+  x = fmaxf(x, dpp_mov<0x4E>(x));    // quad_perm [2,3,0,1]
+  x = fmaxf(x, dpp_mov<0x141>(x));   // row_half_mirror
+  if (G == 16) x = fmaxf(x, dpp_mov<0x140>(x));   // row_mirror
   return x;
 }
 

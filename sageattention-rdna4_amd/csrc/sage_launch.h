@@ -10,8 +10,8 @@ namespace sage {
 // workspace is sized for head_dim 128, which covers 64.
 //   stats pass: grid (C1, BH), each block owns R1 consecutive rows of one plane;
 //   quant pass: grid (ceil(N_pad/R2), BH), each block owns R2 rows.
-// Blocks are sized so that small calls still spread over the chip and large calls keep the
-// per-block mean-partial reduction short (C1 partials of 128 fp64 per plane).
+// Each grid is one round of resident blocks on MI355X (prologue.hip), so C1 stays small and the
+// quant blocks' reduction of the C1 mean partials (128 fp64 each) stays short.
 struct PrologueGeom {
   int64_t R1, C1, R2, C2;
 };
