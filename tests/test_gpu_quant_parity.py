@@ -261,3 +261,21 @@ def test_quant_q_d64_bit_exact(dtype, qk_int8, N):
     r8, rsq, rcq = oracle.quant_q(q.reshape(3, N, 64), sm, int8=qk_int8)
     assert bytes_equal(q8.cpu(), r8), mismatch_report(q8.cpu(), r8, "q8")
     assert bytes_equal(sq.cpu(), rsq) and bytes_equal(cq.cpu(), rcq)
+
+
+@pytest.mark.parametrize("dtype,k_int8,B,H,N", [
+    (torch.float16, True, 20, 40, 70),      # 800 planes: one stats block per plane (768 slots)
+    (torch.bfloat16, False, 40, 60, 33),    # 2400 planes: one quant block per plane too (2048)
+    (torch.float16, True, 1, 1, 5000),      # one plane over 40 stats / 79 quant blocks
+], ids=["BH800", "BH2400", "BH1-N5000"])
+def test_prologue_grid_regimes(dtype, k_int8, B, H, N):
+    # The prologue's grids are sized to one round of resident blocks: c = slots / planes blocks per
+    # plane, at least one. Each regime must give the oracle's bits (and fill every pad row).
+    q, k, v = make_qkv(B, H, N, seed=B * H + N, dtype=dtype, k_offset_std=2.0)
+    v[0, 0, N // 2] = 3000.0                 # S > 1 on one plane
+    print("grid regime", B, H, N, flush=True)
+    ref = _oracle_prologue(k, v, k_int8=k_int8, smooth_k=True)
+    got = _run_prologue(k.cuda(), v.cuda(), k_int8=k_int8, smooth_k=True, fold=True)
+    assert bytes_equal(got["mean"], ref["mean"]), mismatch_report(got["mean"], ref["mean"], "mean")
+    for name, rname in (("k8", "k8"), ("sk", "sk"), ("v8t", "v8t"), ("sv", "svp"), ("s", "s")):
+        assert bytes_equal(got[name], ref[rname]), mismatch_report(got[name], ref[rname], name)
