@@ -331,6 +331,18 @@ __device__ __forceinline__ void rescale_acc(f32x16 (&acc)[NDT], float alpha) {
   }
 }
 
+// 64 wait states before VALU code reads accumulators that P.V MFMAs may have just written (the
+// epilogue). The compiler's own padding after v_mfma_scale_f32_32x32x64_f8f6f4 is 18 wait states,
+// short of what the hardware takes to write the last pass of the result: in a main-loop variant
+// whose last P.V was followed by register copies, a copy of registers 14-15 of the final tile made
+// 18 wait states after the MFMA read stale values, nondeterministically (output channels 122,
+// 123, 126 and 127).
+__device__ __forceinline__ void mfma_result_fence() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // probs_block: p = exp2(c_q*x - mc); l = l*alpha + sum p (the row sum is taken before the fold);
 // P8 = e4m3(p * RN(SV'*448)) into pb; with RESCALE, acc *= alpha (else the caller does it before
 // the block's P.V). Independent steps: the throughput-bound half. w0/w1: the W broadcast sources.

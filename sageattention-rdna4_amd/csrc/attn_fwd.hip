@@ -202,6 +202,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(attn_waves(D
   // of it (an MFMA under a partial EXEC mask loses the inactive lanes' operand rows).
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) keep_live(acc[dt]);
+  mfma_result_fence();
 
   // ---------- epilogue: O = acc * S / (l * 448) (+ V's mean with smooth_v, one fma) ----------
   if (qrow < N) {

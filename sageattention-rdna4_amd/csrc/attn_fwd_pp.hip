@@ -269,6 +269,7 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
   // (an MFMA under a partial EXEC mask loses the inactive lanes' operand rows).
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) asm volatile("" ::"v"(acc[dt]));
+  mfma_result_fence();
 
   // ---------- epilogue: O = acc * S / (l * 448) (+ V's mean with smooth_v, one fma) ----------
   if (qrow < N) {
