@@ -20,7 +20,7 @@
 //
 // Thread layout of both passes: 256 threads = 16 column groups (cg, 8 columns = one 16-byte load)
 // x 16 row groups (rg). The 16 lanes sharing a row are one aligned 16-lane group of a wave, so a
-// row's absmax is a 4-step xor shuffle.
+// row's absmax is four DPP max steps within the group (maxg).
 #include "sage_device.h"
 #include "sage_launch.h"
 
