@@ -207,9 +207,9 @@ def main():
     ap.add_argument("--workload", default="c3c", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
-    ap.add_argument("--kernel", type=int, default=0, choices=(0, 1, 2),
+    ap.add_argument("--kernel", type=int, default=0, choices=(0, 1, 2, 3),
                     help="main-loop kernel: 0 by size (the library's default), 1 the 128-query "
-                         "kernel, 2 the 256-query ping-pong")
+                         "kernel, 2 the 256-query ping-pong, 3 the pipelined 128-query kernel")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of the benchmark, run a plain device copy of this many MiB "
                          "(the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -237,7 +237,8 @@ def main():
     # the library's choice by size (sage_attn_fwd_ex): 256 queries per block from N = 32768 on,
     # head_dim 128 only
     q256 = args.kernel == 2 or (args.kernel == 0 and N >= 32768 and D == 128)
-    kname = "attn_fwd_pp_kernel" if q256 else "attn_fwd_kernel"
+    kname = ("attn_fwd_pl_kernel" if args.kernel == 3 else
+             "attn_fwd_pp_kernel" if q256 else "attn_fwd_kernel")
     for _ in range(args.warmup):
         call()
     torch.cuda.synchronize()

@@ -39,6 +39,7 @@ extern "C" {
 #define SAGE_KERNEL_AUTO 0  /* by size: the 256-query ping-pong from N = 32768 on, else 128 */
 #define SAGE_KERNEL_Q128 1  /* 128 queries per block of 4 waves */
 #define SAGE_KERNEL_Q256 2  /* 256 queries per block of 8 waves, two groups in ping-pong */
+#define SAGE_KERNEL_PIPE 3  /* 128 queries per block of 4 waves, MFMAs pipelined inside each wave */
 
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
 int sage_version(void);

@@ -342,6 +342,20 @@ __device__ __forceinline__ void mfma_result_fence() {
   asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
 }
+// The same for the duration of the 32x32x32 int8 MFMA (32 wait states), or of the MFMA that
+// computed S^T: int8 Q.K (32) or e4m3 Q.K (64).
+__device__ __forceinline__ void mfma_result_fence32() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 15\n\ts_nop 15" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+template <bool QK_INT8>
+__device__ __forceinline__ void qk_result_fence() {
+  if (QK_INT8)
+    mfma_result_fence32();
+  else
+    mfma_result_fence();
+}
 
 // probs_block: p = exp2(c_q*x - mc); l = l*alpha + sum p (the row sum is taken before the fold);
 // P8 = e4m3(p * RN(SV'*448)) into pb; with RESCALE, acc *= alpha (else the caller does it before

@@ -171,6 +171,11 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(attn_waves(D
       const KeyConsts kc = load_key_consts(sc, lane);
       f32x16 st[2];
       qk_block<QK_INT8, D>(kcur, qf, krow0, krow1, ksw0, ksw1, hh, st);
+      // the softmax reads S^T right away: wait out the MFMA's duration first (the compiler's
+      // own padding after these MFMAs is shorter than what the hardware was measured to need)
+      keep_live(st[0]);
+      keep_live(st[1]);
+      qk_result_fence<QK_INT8>();
       i32x8 pb;
       softmax_block<QK_INT8, CAUSAL>(st, kc, j, q0, qrow, Nk, hh, cq, m_x, mc, l_i, acc, pb);
 
@@ -292,6 +297,7 @@ __global__ __launch_bounds__(64) void layout_probe_kernel(const u8* __restrict__
 #pragma unroll
   for (int i = 0; i < 16; ++i) d[i] = 0.0f;
   d = mfma_f8(e, ft, d);
+  mfma_result_fence();   // the stores below read the results
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int row = 8 * (i >> 2) + 4 * h + (i & 3);

@@ -129,26 +129,31 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
     qk_block<QK_INT8>(sB[P].k, qf, krow0, krow1, ksw0, ksw1, hh, st);
   };
   float alpha_pend = 1.0f;      // alpha of the block whose P.V comes next
-  auto pv = [&](auto par) {
-    constexpr int P = decltype(par)::value;
+  // P.V of the block whose V^T tile is in buffer p (a compile-time index inside the unrolled
+  // loop, a run-time one for the drain after it)
+  auto pv_buf = [&](int p) {
     rescale_acc(acc, alpha_pend);
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
-      const u8* vb = &sB[P].v[(32 * dt + vrow) * BK];
+      const u8* vb = &sB[p].v[(32 * dt + vrow) * BK];
       const i32x4 lo = *(const i32x4*)(vb + 16 * ((2 * hh) ^ vsw));
       const i32x4 hi = *(const i32x4*)(vb + 16 * ((2 * hh + 1) ^ vsw));
       const i32x8 vf = (i32x8){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
       acc[dt] = mfma_f8(vf, pb, acc[dt]);
     }
   };
-  auto pv_rt = [&](int j) {    // P.V of block j, buffer chosen at run time (uniform branch)
-    const int p = j % 3;
-    if (p == 0)
-      pv(I0{});
-    else if (p == 1)
-      pv(I1{});
-    else
-      pv(I2{});
+  auto pv = [&](auto par) { pv_buf(decltype(par)::value); };
+  auto pin_acc = [&]() {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) asm volatile("" ::"v"(acc[dt]));
+  };
+  // P.V of block j after the loop, the buffer indexed at run time: one code path, so that the
+  // accumulators are not moved between register ranges at a branch join right after the MFMAs
+  // (such copies read the MFMA results before the hardware has written them)
+  auto pv_rt = [&](int j) {
+    pv_buf(j % 3);
+    pin_acc();
+    mfma_result_fence();
   };
   // softmax of block j on st with its constants, read into registers one phase ahead (during
   // the wave's MFMA phase); the P.V of block j-1 has already been issued
@@ -167,10 +172,6 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
   };
   // A phase's products are pinned before its barrier: without the pins the compiler is free to
   // sink MFMAs (which touch no memory) past the barrier into the next phase.
-  auto pin_acc = [&]() {
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) asm volatile("" ::"v"(acc[dt]));
-  };
   auto pin_st = [&]() { asm volatile("" ::"v"(st[0]), "v"(st[1])); };
   auto pin_pb = [&]() { asm volatile("" ::"v"(pb)); };
   auto end_phase1 = [&](bool more2) {
@@ -195,6 +196,8 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
     // group A: phase 1 softmax(j); phase 2 P.V(j), then S^T(j+1) (computed also after the last
     // block, from whatever buffer j+1 holds, and never used: it keeps S^T's live range simple).
     qk(I0{});
+    pin_st();
+    mfma_result_fence();
     prefetch_consts(I0{});
     auto blk = [&](const int jj, auto par) {
       constexpr int P = decltype(par)::value;
@@ -206,8 +209,12 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
       end_phase1(more2);
       if (more2) dma_vc(jj + 2, PF);
       prefetch_consts(std::integral_constant<int, PN>{});   // landed at the barrier above
-      pv(par);
+      // S^T first, P.V after it: the P.V MFMAs then hold this wave's issue until S^T has been
+      // written, before the barrier ahead of the softmax that reads it
       qk(std::integral_constant<int, PN>{});
+      pin_st();
+      __builtin_amdgcn_sched_barrier(0);
+      pv(par);
       pin_acc();
       pin_st();
       end_phase2();
@@ -221,6 +228,7 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
       blk(j, I0{});
       if (j + 1 < w_end) blk(j + 1, I1{});
     }
+    mfma_result_fence();   // the last P.V's results are next read after the loop
   } else {
     // group B: phase 1 P.V(j-1), then S^T(j); phase 2 softmax(j).
     auto blk = [&](const int jj, auto par, auto first) {
@@ -229,10 +237,17 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
       const bool more2 = jj + 2 < j_end;
       if (more2) dma_k(jj + 2, PF);
       prefetch_consts(par);
-      if constexpr (!decltype(first)::value) pv(std::integral_constant<int, PF>{});
       qk(par);
-      pin_acc();
       pin_st();
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (!decltype(first)::value) {
+        pv(std::integral_constant<int, PF>{});   // after S^T, as in group A
+        pin_acc();
+        pin_st();
+      } else {
+        pin_st();
+        mfma_result_fence();   // no P.V behind S^T in the first block
+      }
       end_phase1(more2);
       if (more2) dma_vc(jj + 2, PF);
       softmax(jj);
@@ -256,10 +271,7 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
     const bool more2 = j + 2 < j_end;
     const int pf = (j + 2) % 3;
     if (more2) dma_k(j + 2, pf);
-    if (g == 1 && j == w_end) {
-      pv_rt(j - 1);
-      pin_acc();
-    }
+    if (g == 1 && j == w_end) pv_rt(j - 1);
     end_phase1(more2);
     if (more2) dma_vc(j + 2, pf);
     end_phase2();

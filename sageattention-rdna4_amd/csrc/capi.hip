@@ -165,7 +165,8 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
     return fail(SAGE_ERR_INVALID, "ptr_align: quantized inputs must be 16-byte aligned");
   if (!(sm_scale > 0.0f) || !(sm_scale < 3.0e38f))
     return fail(SAGE_ERR_INVALID, "sm_scale: must be positive and finite (got %g)", (double)sm_scale);
-  if (kernel != SAGE_KERNEL_AUTO && kernel != SAGE_KERNEL_Q128 && kernel != SAGE_KERNEL_Q256)
+  if (kernel != SAGE_KERNEL_AUTO && kernel != SAGE_KERNEL_Q128 && kernel != SAGE_KERNEL_Q256 &&
+      kernel != SAGE_KERNEL_PIPE)
     return fail(SAGE_ERR_INVALID, "kernel: unknown main-loop kernel code %d", kernel);
   if (lse && ((uintptr_t)lse & 3u))
     return fail(SAGE_ERR_INVALID, "ptr_align: lse must be 4-byte aligned");
@@ -183,6 +184,8 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
   a.q_sr = q_sr;
   a.k8 = k8;
   a.kconst = kconst;
+  a.sk = nullptr;
+  a.svp = nullptr;
   a.v8t = v8t;
   a.s = s;
   a.o = o;
@@ -205,6 +208,8 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
   // SIMD) is faster: measured 3 % faster at N = 16384, 3 % slower at N = 47520.
   const bool q256 = kernel == SAGE_KERNEL_Q256 ||
                     (kernel == SAGE_KERNEL_AUTO && D == 128 && N >= 32768 && N_kv >= 32768);
+  if (kernel == SAGE_KERNEL_PIPE)
+    return hip_status(sage::launch_attn_fwd_pl(a, (hipStream_t)stream), "sage_attn_fwd launch");
   return hip_status(q256 ? sage::launch_attn_fwd_pp(a, (hipStream_t)stream)
                          : sage::launch_attn_fwd(a, (hipStream_t)stream),
                     "sage_attn_fwd launch");

@@ -43,7 +43,9 @@ struct AttnArgs {
   const void* q;
   int64_t q_sb, q_sh, q_sr;
   const void* k8;
-  const float* kconst;
+  const float* kconst;      // per-key constants in the prologue's KCONST layout, or NULL and:
+  const float* sk;          //   SK (B*H_kv, N_kv_pad) and
+  const float* svp;         //   SV' (B*H_kv, N_kv_pad), the reference's arrays
   const void* v8t;
   const float* s;
   void* o;
@@ -59,6 +61,8 @@ struct AttnArgs {
 hipError_t launch_attn_fwd(const AttnArgs& a, hipStream_t stream);
 // the two-group ping-pong form of the same main loop (256 queries per block of 8 waves)
 hipError_t launch_attn_fwd_pp(const AttnArgs& a, hipStream_t stream);
+// the software-pipelined form (128 queries per block of 4 waves, three or four blocks per CU)
+hipError_t launch_attn_fwd_pl(const AttnArgs& a, hipStream_t stream);
 
 struct QuantQArgs {
   int dtype, qk_int8;

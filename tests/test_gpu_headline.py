@@ -1,8 +1,16 @@
-"""Parity at the benchmark's own sequence lengths (GPU tests), one head each so that the CPU
-emulation finishes in seconds: the headline c3c (fp16, N = 47520, causal, int8 Q.K, the 256-query
-kernel) and c4 (bf16, N = 16384, causal, e4m3 Q.K, the 128-query kernel), on the configurations'
-synthetic inputs. The prologue's quantized tensors must equal the oracle's byte for byte and the
-output must reach cos >= 0.999 and rel-L1 <= 1e-2 against the emulation.
+"""Parity at the benchmark's own sequence lengths (GPU tests), on the configurations' synthetic
+inputs, with heads (and batch) capped so that the CPU emulation finishes in seconds:
+
+* c3c: fp16, N = 47520, causal (int8 Q.K, the 256-query kernel by the size rule);
+* c3n: fp16, N = 47520, non-causal (the 256-query kernel, non-causal: every key block of every
+  query tile, tail masks on the last block);
+* c4: bf16, N = 16384, causal (e4m3 Q.K, the 128-query kernel);
+* c5_4096: fp16, N = 4096 at the B1 H48 shape's per-head work (4 heads), non-causal, no K offset;
+* c5_b8: fp16, B = 8, H = 24, N = 4096, NHD (batch capped at 2 and heads at 4; the NHD strides
+  (H*D, D, N*H*D) are the real call's).
+
+The prologue's quantized tensors must equal the oracle's byte for byte and the output must reach
+cos >= 0.999 and rel-L1 <= 1e-2 against the emulation.
 """
 import pytest
 import torch
@@ -15,20 +23,23 @@ pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not have_gfx950(), reason="needs a gfx950 GPU")]
 
 
-@pytest.mark.parametrize("name,dtype,N,outliers,std", [
-    ("c3c", torch.float16, 47520, 0.0, 1.0),
-    ("c4", torch.bfloat16, 16384, 0.001, 1.5),
+@pytest.mark.parametrize("name,dtype,B,H,N,causal,layout,k_off,outliers,std", [
+    ("c3c", torch.float16, 1, 1, 47520, True, "HND", 2.0, 0.0, 1.0),
+    ("c3n", torch.float16, 1, 1, 47520, False, "HND", 2.0, 0.0, 1.0),
+    ("c4", torch.bfloat16, 1, 1, 16384, True, "HND", 2.0, 0.001, 1.5),
+    ("c5_4096", torch.float16, 1, 4, 4096, False, "HND", 0.0, 0.0, 1.0),
+    ("c5_b8", torch.float16, 2, 4, 4096, False, "NHD", 0.0, 0.0, 1.0),
 ])
-def test_benchmark_length_parity(name, dtype, N, outliers, std):
+def test_benchmark_length_parity(name, dtype, B, H, N, causal, layout, k_off, outliers, std):
     from sageattention import sageattn
-    q, k, v = make_qkv(1, 1, N, seed=0, dtype=dtype, std=std, k_offset_std=2.0,
+    q, k, v = make_qkv(B, H, N, seed=0, dtype=dtype, layout=layout, std=std, k_offset_std=k_off,
                        outlier_frac=outliers)
-    print("case", name, N, flush=True)
-    assert quantized_bit_exact(k, v, "HND", k_int8=(dtype == torch.float16))
-    out = sageattn(q.cuda(), k.cuda(), v.cuda(), tensor_layout="HND", is_causal=True)
+    print("case", name, B, H, N, causal, layout, flush=True)
+    assert quantized_bit_exact(k, v, layout, k_int8=(dtype == torch.float16))
+    out = sageattn(q.cuda(), k.cuda(), v.cuda(), tensor_layout=layout, is_causal=causal)
     torch.cuda.synchronize()
-    emu = oracle.emulate_sageattn(q, k, v, is_causal=True)["o"]
+    emu = oracle.emulate_sageattn(q, k, v, tensor_layout=layout, is_causal=causal)["o"]
     out = out.cpu()
-    assert torch.isfinite(out).all()
+    assert out.shape == q.shape and torch.isfinite(out).all()
     c, r = cosine(out, emu), rel_l1(out, emu)
     assert c >= 0.999 and r <= 1e-2, (c, r)
