@@ -35,7 +35,7 @@ extern "C" {
 #define SAGE_F16 0
 #define SAGE_BF16 1
 
-/* main-loop kernel choice of sage_attn_fwd_ex */
+/* main-loop kernel choice of sage_attn_fwd_ex (all give the same bits) */
 #define SAGE_KERNEL_AUTO 0  /* by size: the 256-query ping-pong from N = 32768 on, else 128 */
 #define SAGE_KERNEL_Q128 1  /* 128 queries per block of 4 waves */
 #define SAGE_KERNEL_Q256 2  /* 256 queries per block of 8 waves, two groups in ping-pong */
@@ -48,11 +48,23 @@ int sage_version(void);
 const char* sage_last_error(void);
 
 /*
- * Bytes of device workspace `sage_kv_prologue` needs for B*H planes of N rows.
- * No reference counterpart: the reference allocates its mean with torch per call
- * (`sageattention/sk1_backend/hip_prologue.py:219-222`).
+ * Bytes of device workspace `sage_kv_prologue` (and `sage_kseq_mean`) needs for B*H planes of N
+ * rows, for any N_pad. No reference counterpart: the reference allocates its mean with torch per
+ * call (`sageattention/sk1_backend/hip_prologue.py:219-222`).
  */
 size_t sage_kv_prologue_workspace_bytes(int64_t BH, int64_t N);
+
+/*
+ * The smooth_k sequence mean alone: MEAN (B*H, D) fp32 = fp32(sum_n fp64(k[n,d]) / N), the same
+ * bits as the `mean` output of sage_kv_prologue (same partial sums, same order). Two launches.
+ * Replaces `HipPrologue.kseq_mean` / `h34_kseq_mean_{f16,bf16}`
+ * (`sageattention/sk1_backend/hip_prologue.py:267-292`; `kernels/hip/h34_prologue.hip:259-294`).
+ *   k          logical (B, H, N, D) view, D = 64 or 128, element strides (k_sb, k_sh, k_sr)
+ *   workspace  at least sage_kv_prologue_workspace_bytes(B*H, N) bytes, 256-byte aligned
+ */
+int sage_kseq_mean(int dtype, const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sr,
+                   int64_t B, int64_t H, int64_t N, int64_t D, float* mean, void* workspace,
+                   size_t workspace_bytes, void* stream);
 
 /*
  * The K/V prologue: smooth_k mean, per-token K (int8 or fp8) and V (fp8) quantization, and the
@@ -151,6 +163,30 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal,
                      int64_t B, int64_t H, int64_t N, int64_t H_kv, int64_t N_kv,
                      int64_t N_kv_pad, int64_t D, float sm_scale, int kernel,
                      float* lse, const float* kmean, const float* vmean, void* stream);
+
+/*
+ * The main loop on the reference kernel's own inputs: per-key scales SK (B*H_kv, N_kv_pad) and
+ * folded value scales SV' (B*H_kv, N_kv_pad) fp32, as the reference's attention kernels take them
+ * (`kernels/hip/sk1_t6i.hip:302-306`, `kernels/hip/sk1_t6in.hip:314-320`; the contract of
+ * `Sk1Attn._check`, `sageattention/sk1_backend/sk1_loader.py:405-442`), instead of the prologue's
+ * KCONST layout. W = RN(SV' * 448) is formed in the kernel with the same single rounding the
+ * prologue applies, so for the prologue's SK and SV' the output equals sage_attn_fwd_ex's bit
+ * for bit. Runs the software-pipelined kernel (SAGE_KERNEL_PIPE) at every size.
+ *   k8, sk, v8t, sv, s   K8, SK, V8T, SV' and S of the scheme for B*H_kv planes of N_kv keys;
+ *                        sk and sv 16-byte aligned
+ *   vmean                optional (B*H_kv, D) fp32 added to the output (the reference kernel's
+ *                        VMEAN, `kernels/hip/sk1_t6i.hip:290-297`)
+ *   lse, kmean           as in sage_attn_fwd_ex
+ * Other arguments as in sage_attn_fwd_ex.
+ */
+int sage_attn_fwd_sk(int dtype, int qk_int8, int causal,
+                     const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sr,
+                     const void* k8, const float* sk, const void* v8t, const float* sv,
+                     const float* vmean, const float* s,
+                     void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr,
+                     int64_t B, int64_t H, int64_t N, int64_t H_kv, int64_t N_kv,
+                     int64_t N_kv_pad, int64_t D, float sm_scale,
+                     float* lse, const float* kmean, void* stream);
 
 /*
  * Q quantization exactly as the main loop performs it, written out for parity checks.

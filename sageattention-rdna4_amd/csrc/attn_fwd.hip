@@ -240,16 +240,18 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(attn_waves(D
 
 // ---------------------------------------------------------------------------------------------
 // Parity entry: Q quantization exactly as the main loop does it, written out.
-// grid (ceil(N/32), BH), block 64: lane (q, h) of the wave handles row 32*blockIdx.x + q.
+// 1-D grid of ceil(N/32) * BH blocks of 64 threads: block bh * ceil(N/32) + t, lane (q, h) of the
+// wave handles row 32 t + q of plane bh.
 // ---------------------------------------------------------------------------------------------
 template <typename T, bool QK_INT8, int D>
 __global__ __launch_bounds__(64) void quant_q_kernel(const T* __restrict__ Q, int64_t q_sb,
                                                      int64_t q_sh, int64_t q_sr, int H, int N,
                                                      float sm_scale, u8* __restrict__ Q8,
                                                      float* __restrict__ SQ, float* __restrict__ CQ) {
-  const int bh = blockIdx.y, b = bh / H, hd = bh - b * H;
+  const int nqb = (N + 31) / 32;
+  const int bh = blockIdx.x / nqb, b = bh / H, hd = bh - b * H;
   const int lane = threadIdx.x, l32 = lane & 31, hh = lane >> 5;
-  const int qrow = blockIdx.x * 32 + l32;
+  const int qrow = (blockIdx.x - bh * nqb) * 32 + l32;
   QFrag<D> qf;
   float sq, cq;
   quant_q_row<T, QK_INT8, D>(Q + b * q_sb + hd * q_sh + (int64_t)qrow * q_sr, qrow < N, hh,
@@ -351,7 +353,7 @@ hipError_t launch_attn_fwd(const AttnArgs& a, hipStream_t stream) {
 
 template <typename T, bool QK_INT8, int D>
 static void launch_quant_q_t(const QuantQArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)((a.N + 31) / 32), (unsigned)(a.B * a.H));
+  const dim3 grid((unsigned)((a.N + 31) / 32 * a.B * a.H));
   hipLaunchKernelGGL((quant_q_kernel<T, QK_INT8, D>), grid, dim3(64), 0, stream, (const T*)a.q,
                      a.q_sb, a.q_sh, a.q_sr, (int)a.H, (int)a.N, a.sm_scale, (u8*)a.q8, a.sq,
                      a.cq);

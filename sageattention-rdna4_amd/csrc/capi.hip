@@ -55,7 +55,10 @@ int check_shape(int64_t B, int64_t H, int64_t N, int64_t N_pad) {
   if (N_pad < N || (N_pad % 64) != 0)
     return fail(SAGE_ERR_INVALID, "n_pad: N_pad must be a multiple of 64 and >= N (N=%lld N_pad=%lld)",
                 (long long)N, (long long)N_pad);
-  if (B * H > 65535 || N_pad > kInt32Max / 128 || B * H * ((N + 127) / 128) > kInt32Max)
+  // Grids are 1-D lists of (plane, tile) blocks, so B*H itself has no limit of its own; the
+  // 128-row tiles of every plane must fit one int32 block index, and a plane's padded rows the
+  // 32-bit in-plane offsets of the main loop's staging.
+  if (N_pad > kInt32Max / 128 || B * H * ((N + 127) / 128) > kInt32Max)
     return fail(SAGE_ERR_INVALID, "shape too large for the grid (B*H=%lld N=%lld)",
                 (long long)(B * H), (long long)N);
   return SAGE_OK;
@@ -77,7 +80,7 @@ const char* sage_last_error(void) { return g_err.c_str(); }
 
 size_t sage_kv_prologue_workspace_bytes(int64_t BH, int64_t N) {
   if (BH < 1 || N < 1) return 0;
-  return sage::prologue_workspace_bytes(BH, (N + 63) / 64 * 64);
+  return sage::prologue_workspace_bytes(BH, N);
 }
 
 int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int smooth_v, int fold, const void* k,
@@ -101,7 +104,7 @@ int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int smooth_v, int fold
     return fail(SAGE_ERR_INVALID, "vmean: smooth_v needs the vmean output (B*H x 128 fp32)");
   if (!aligned16(k8) || !aligned16(v8t) || !aligned16(sk) || !aligned16(sv) || !aligned16(kconst))
     return fail(SAGE_ERR_INVALID, "ptr_align: outputs must be 16-byte aligned");
-  const size_t need = sage::prologue_workspace_bytes(B * H, N_pad);
+  const size_t need = sage::prologue_workspace_bytes(B * H, N);
   if (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 255u))
     return fail(SAGE_ERR_INVALID, "workspace: need %zu bytes, 256-byte aligned (got %zu)", need,
                 workspace_bytes);
@@ -215,6 +218,105 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
                     "sage_attn_fwd launch");
 }
 
+int sage_attn_fwd_sk(int dtype, int qk_int8, int causal, const void* q, int64_t q_sb,
+                     int64_t q_sh, int64_t q_sr, const void* k8, const float* sk,
+                     const void* v8t, const float* sv, const float* vmean, const float* s,
+                     void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr, int64_t B, int64_t H,
+                     int64_t N, int64_t H_kv, int64_t N_kv, int64_t N_kv_pad, int64_t D,
+                     float sm_scale, float* lse, const float* kmean, void* stream) {
+  if (dtype != SAGE_F16 && dtype != SAGE_BF16)
+    return fail(SAGE_ERR_INVALID, "dtype: unsupported dtype code %d", dtype);
+  if (dtype == SAGE_BF16 && qk_int8)
+    return fail(SAGE_ERR_INVALID, "bf16_int8: int8 Q.K is served for fp16 inputs only");
+  int rc = check_shape(B, H, N, (N + 63) / 64 * 64);
+  if (rc) return rc;
+  if (H_kv < 1 || H % H_kv != 0)
+    return fail(SAGE_ERR_INVALID, "heads: H (%lld) must be a multiple of H_kv (%lld)",
+                (long long)H, (long long)H_kv);
+  if ((rc = check_shape(B, H_kv, N_kv, N_kv_pad))) return rc;
+  if (causal && N != N_kv)
+    return fail(SAGE_ERR_INVALID, "seq_len: causal attention needs N == N_kv (N=%lld N_kv=%lld)",
+                (long long)N, (long long)N_kv);
+  if ((rc = check_head_dim(D))) return rc;
+  if ((rc = check_view("q", q, q_sb, q_sh, q_sr))) return rc;
+  if ((rc = check_view("o", o, o_sb, o_sh, o_sr))) return rc;
+  if (!k8 || !sk || !v8t || !sv || !s) return fail(SAGE_ERR_INVALID, "an input pointer is NULL");
+  // the per-key rows are staged 256 bytes per 64-key block
+  if (!aligned16(k8) || !aligned16(v8t) || !aligned16(sk) || !aligned16(sv))
+    return fail(SAGE_ERR_INVALID, "ptr_align: quantized inputs and scales must be 16-byte aligned");
+  if (!(sm_scale > 0.0f) || !(sm_scale < 3.0e38f))
+    return fail(SAGE_ERR_INVALID, "sm_scale: must be positive and finite (got %g)", (double)sm_scale);
+  if (lse && ((uintptr_t)lse & 3u))
+    return fail(SAGE_ERR_INVALID, "ptr_align: lse must be 4-byte aligned");
+  if (kmean && !aligned16(kmean))
+    return fail(SAGE_ERR_INVALID, "ptr_align: kmean must be 16-byte aligned");
+  if (vmean && !aligned16(vmean))
+    return fail(SAGE_ERR_INVALID, "ptr_align: vmean must be 16-byte aligned");
+  sage::AttnArgs a;
+  a.dtype = dtype;
+  a.qk_int8 = qk_int8 ? 1 : 0;
+  a.causal = causal ? 1 : 0;
+  a.q = q;
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.q_sr = q_sr;
+  a.k8 = k8;
+  a.kconst = nullptr;
+  a.sk = sk;
+  a.svp = sv;
+  a.v8t = v8t;
+  a.s = s;
+  a.o = o;
+  a.o_sb = o_sb;
+  a.o_sh = o_sh;
+  a.o_sr = o_sr;
+  a.B = B;
+  a.H = H;
+  a.N = N;
+  a.H_kv = H_kv;
+  a.N_kv = N_kv;
+  a.N_kv_pad = N_kv_pad;
+  a.D = D;
+  a.sm_scale = sm_scale;
+  a.lse = lse;
+  a.kmean = lse ? kmean : nullptr;
+  a.vmean = vmean;
+  return hip_status(sage::launch_attn_fwd_pl(a, (hipStream_t)stream), "sage_attn_fwd_sk launch");
+}
+
+int sage_kseq_mean(int dtype, const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sr,
+                   int64_t B, int64_t H, int64_t N, int64_t D, float* mean, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  if (dtype != SAGE_F16 && dtype != SAGE_BF16)
+    return fail(SAGE_ERR_INVALID, "mean_dtype: unsupported dtype code %d", dtype);
+  const int64_t N_pad = (N + 63) / 64 * 64;
+  int rc = check_shape(B, H, N, N_pad);
+  if (rc) return rc;
+  if (D != 64 && D != 128)
+    return fail(SAGE_ERR_INVALID, "mean_head_dim: D must be 64 or 128 (got %lld)", (long long)D);
+  if ((rc = check_view("k", k, k_sb, k_sh, k_sr))) return rc;
+  if (!mean) return fail(SAGE_ERR_INVALID, "an output pointer is NULL");
+  const size_t need = sage::prologue_workspace_bytes(B * H, N);
+  if (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 255u))
+    return fail(SAGE_ERR_INVALID, "workspace: need %zu bytes, 256-byte aligned (got %zu)", need,
+                workspace_bytes);
+  sage::PrologueArgs a = {};
+  a.dtype = dtype;
+  a.smooth_k = 1;
+  a.k = k;
+  a.k_sb = k_sb;
+  a.k_sh = k_sh;
+  a.k_sr = k_sr;
+  a.B = B;
+  a.H = H;
+  a.N = N;
+  a.N_pad = N_pad;
+  a.D = D;
+  a.mean = mean;
+  a.workspace = workspace;
+  return hip_status(sage::launch_kseq_mean(a, (hipStream_t)stream), "sage_kseq_mean launch");
+}
+
 int sage_attn_fwd(int dtype, int qk_int8, int causal, const void* q, int64_t q_sb, int64_t q_sh,
                   int64_t q_sr, const void* k8, const float* kconst, const void* v8t,
                   const float* s, void* o, int64_t o_sb, int64_t o_sh, int64_t o_sr, int64_t B,
@@ -233,6 +335,9 @@ int sage_quant_q(int dtype, int qk_int8, const void* q, int64_t q_sb, int64_t q_
     return fail(SAGE_ERR_INVALID, "bf16_int8: int8 Q is served for fp16 inputs only");
   int rc = check_shape(B, H, N, (N + 63) / 64 * 64);
   if (rc) return rc;
+  if (B * H * ((N + 31) / 32) > kInt32Max)
+    return fail(SAGE_ERR_INVALID, "shape too large for the grid (B*H=%lld N=%lld)",
+                (long long)(B * H), (long long)N);
   if ((rc = check_head_dim(D))) return rc;
   if ((rc = check_view("q", q, q_sb, q_sh, q_sr))) return rc;
   if (!q8 || !sq || !cq) return fail(SAGE_ERR_INVALID, "an output pointer is NULL");

@@ -47,12 +47,13 @@ constexpr int64_t MI355_CUS = 256;
 constexpr int64_t STATS_BLOCKS_PER_CU = 3;
 constexpr int64_t QUANT_BLOCKS_PER_CU = 8;
 
-PrologueGeom prologue_geom(int64_t BH, int64_t N_pad, int64_t step) {
+PrologueGeom prologue_geom(int64_t BH, int64_t N, int64_t N_pad, int64_t step) {
   auto cdiv = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
   auto blocks_per_plane = [&](int64_t slots) { return BH < slots ? slots / BH : (int64_t)1; };
+  const int64_t Nc = cdiv(N, 64) * 64;
   PrologueGeom g;
-  g.R1 = cdiv(cdiv(N_pad, blocks_per_plane(MI355_CUS * STATS_BLOCKS_PER_CU)), step) * step;
-  g.C1 = cdiv(N_pad, g.R1);
+  g.R1 = cdiv(cdiv(Nc, blocks_per_plane(MI355_CUS * STATS_BLOCKS_PER_CU)), step) * step;
+  g.C1 = cdiv(Nc, g.R1);
   g.R2 = cdiv(cdiv(N_pad, blocks_per_plane(MI355_CUS * QUANT_BLOCKS_PER_CU)), 64) * 64;
   g.C2 = cdiv(N_pad, g.R2);
   return g;
@@ -64,8 +65,9 @@ static size_t part_region_bytes(int64_t BH, const PrologueGeom& g) {
   return ((size_t)BH * g.C1 * HD * sizeof(double) + 255) / 256 * 256;
 }
 
-size_t prologue_workspace_bytes(int64_t BH, int64_t N_pad) {
-  const PrologueGeom g = prologue_geom(BH, N_pad);
+size_t prologue_workspace_bytes(int64_t BH, int64_t N) {
+  const int64_t Nc = (N + 63) / 64 * 64;
+  const PrologueGeom g = prologue_geom(BH, N, Nc);
   const size_t smax = (size_t)BH * g.C1 * sizeof(float);
   return 2 * part_region_bytes(BH, g) + ((smax + 255) / 256 * 256);
 }
@@ -81,7 +83,8 @@ size_t prologue_workspace_bytes(int64_t BH, int64_t N_pad) {
 // V_SUMS: K's and V's mean partials only (smooth_v, first launch).
 // V_CENTERED: V's mean from its partials (written to VMEAN), V - mean quantized (smooth_v, second
 //             launch; K is not read).
-enum VMode { V_QUANT = 0, V_SUMS = 1, V_CENTERED = 2 };
+// K_ONLY: K's mean partials only (the smooth_k mean on its own; V is not read).
+enum VMode { V_QUANT = 0, V_SUMS = 1, V_CENTERED = 2, K_ONLY = 3 };
 
 template <typename T, int VMODE, int D>
 __global__ __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(STATS_BLOCKS_PER_CU))) void kv_stats_kernel(
@@ -97,14 +100,20 @@ __global__ __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(STATS_BLOCKS
   __shared__ float vmu_s[D];
 
   const int tid = threadIdx.x, cg = tid % G::CG, rg = tid / G::CG;
-  const int64_t c = blockIdx.x, bh = blockIdx.y;
+  // 1-D grid: block = bh * C1 + c (any number of planes)
+  const int64_t bh = blockIdx.x / C1, c = blockIdx.x - bh * C1;
   const int64_t b = bh / H, h = bh - b * H;
   const T* kp = K + b * k_sb + h * k_sh + 8 * cg;
   const T* vp = V + b * v_sb + h * v_sh + 8 * cg;
   u8* vt = V8T + bh * D * N_pad;
   const int64_t r_begin = c * R1;
-  const int64_t r_end = (r_begin + R1 < N_pad) ? r_begin + R1 : N_pad;
-  const bool k_sums = smooth_k && VMODE != V_CENTERED;
+  // the plane's last block also covers the pure pad rows up to N_pad
+  const int64_t r_end = (c == C1 - 1 || r_begin + R1 > N_pad) ? N_pad : r_begin + R1;
+  const bool k_sums = (smooth_k && VMODE != V_CENTERED) || VMODE == K_ONLY;
+  if (VMODE == K_ONLY && r_begin >= N) {   // nothing but pad rows: zero partials
+    if (tid < D) part[(bh * C1 + c) * D + tid] = 0.0;
+    return;
+  }
 
   // V's sequence mean (V_CENTERED): every block of the plane reduces the same partials in the
   // same order, so all of them subtract the same bits.
@@ -133,7 +142,7 @@ __global__ __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(STATS_BLOCKS
     for (int i = 0; i < 8; ++i) {
       const int64_t n = n0 + 8 * rg + i;
       const bool live = n < N;
-      vw[i] = live ? *(const u32x4*)(vp + n * v_sr) : (u32x4){0u, 0u, 0u, 0u};
+      vw[i] = (live && VMODE != K_ONLY) ? *(const u32x4*)(vp + n * v_sr) : (u32x4){0u, 0u, 0u, 0u};
       kw[i] = (live && k_sums) ? *(const u32x4*)(kp + n * k_sr) : (u32x4){0u, 0u, 0u, 0u};
     }
     if (k_sums) {
@@ -155,6 +164,7 @@ __global__ __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(STATS_BLOCKS
       }
       continue;
     }
+    if (VMODE == K_ONLY) continue;
     // V: per-row scale and e4m3 bytes. col_lo/col_hi[e] collect tokens 0..3 / 4..7 of column e.
     uint32_t col_lo[8], col_hi[8];
 #pragma unroll
@@ -242,6 +252,7 @@ __global__ __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(STATS_BLOCKS
     }
     return;   // V is quantized by the V_CENTERED launch
   }
+  if (VMODE == K_ONLY) return;
   // block max of sv over live rows
   float m = sv_max;
 #pragma unroll
@@ -259,7 +270,7 @@ __global__ __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(QUANT_BLOCKS
     const T* __restrict__ K, u8* __restrict__ K8, float* __restrict__ SK, float* __restrict__ SV,
     const double* __restrict__ part, const float* __restrict__ smax, float* __restrict__ MEAN,
     float* __restrict__ S_out, float* __restrict__ KC, int64_t H, int64_t N, int64_t N_pad,
-    int64_t R2, int64_t C1,
+    int64_t R2, int64_t C2, int64_t C1,
     int64_t k_sb, int64_t k_sh, int64_t k_sr, int smooth_k, int fold) {
   using G = Geo<D>;
   constexpr int RG = G::RG;
@@ -267,7 +278,8 @@ __global__ __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(QUANT_BLOCKS
   __shared__ float s_fold;
 
   const int tid = threadIdx.x, cg = tid % G::CG, rg = tid / G::CG;
-  const int64_t bh = blockIdx.y;
+  // 1-D grid: block = bh * C2 + c2 (any number of planes)
+  const int64_t bh = blockIdx.x / C2, c2 = blockIdx.x - bh * C2;
   const int64_t b = bh / H, h = bh - b * H;
 
   if (tid < D) {
@@ -276,7 +288,7 @@ __global__ __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(QUANT_BLOCKS
       double s = 0.0;
       for (int64_t c = 0; c < C1; ++c) s += part[(bh * C1 + c) * D + tid];
       mu = (float)(s / (double)N);
-      if (MEAN != nullptr && blockIdx.x == 0) MEAN[bh * D + tid] = mu;
+      if (MEAN != nullptr && c2 == 0) MEAN[bh * D + tid] = mu;
     }
     mu_s[tid] = mu;
   } else if (tid < D + 64) {
@@ -287,7 +299,7 @@ __global__ __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(QUANT_BLOCKS
     for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
     if (l == 0) {
       s_fold = m;
-      if (blockIdx.x == 0) S_out[bh] = m;
+      if (c2 == 0) S_out[bh] = m;
     }
   }
   __syncthreads();
@@ -297,7 +309,7 @@ __global__ __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(QUANT_BLOCKS
   for (int e = 0; e < 8; ++e) mu[e] = mu_s[8 * cg + e];
   const float S = s_fold;
   const T* kp = K + b * k_sb + h * k_sh + 8 * cg;
-  const int64_t r_begin = (int64_t)blockIdx.x * R2;
+  const int64_t r_begin = c2 * R2;
   const int64_t r_end = (r_begin + R2 < N_pad) ? r_begin + R2 : N_pad;
 
   for (int64_t n0 = r_begin; n0 < r_end; n0 += 64) {
@@ -364,13 +376,13 @@ __global__ __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(QUANT_BLOCKS
 template <typename T, int D>
 static hipError_t launch_prologue_t(const PrologueArgs& a, hipStream_t stream) {
   const int64_t BH = a.B * a.H;
-  const PrologueGeom g = prologue_geom(BH, a.N_pad, Geo<D>::STEP);
+  const PrologueGeom g = prologue_geom(BH, a.N, a.N_pad, Geo<D>::STEP);
   // region offsets as sized for head_dim 128 (prologue_workspace_bytes)
-  const size_t part_bytes = part_region_bytes(BH, prologue_geom(BH, a.N_pad));
+  const size_t part_bytes = part_region_bytes(BH, prologue_geom(BH, a.N, a.N_pad));
   double* part = (double*)a.workspace;
   double* vpart = (double*)((char*)a.workspace + part_bytes);
   float* smax = (float*)((char*)a.workspace + 2 * part_bytes);
-  const dim3 grid1((unsigned)g.C1, (unsigned)BH);
+  const dim3 grid1((unsigned)(g.C1 * BH));
   if (a.smooth_v) {
     // V's mean first (with K's partials), then V - mean quantized
     hipLaunchKernelGGL((kv_stats_kernel<T, V_SUMS, D>), grid1, dim3(PT), 0, stream, (const T*)a.k,
@@ -391,15 +403,53 @@ static hipError_t launch_prologue_t(const PrologueArgs& a, hipStream_t stream) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  const dim3 grid2((unsigned)(g.C2 * BH));
   if (a.k_int8)
-    hipLaunchKernelGGL((k_quant_kernel<T, true, D>), dim3((unsigned)g.C2, (unsigned)BH), dim3(PT), 0,
+    hipLaunchKernelGGL((k_quant_kernel<T, true, D>), grid2, dim3(PT), 0,
                        stream, (const T*)a.k, (u8*)a.k8, a.sk, a.sv, part, smax, a.mean, a.s, a.kconst, a.H,
-                       a.N, a.N_pad, g.R2, g.C1, a.k_sb, a.k_sh, a.k_sr, a.smooth_k, a.fold);
+                       a.N, a.N_pad, g.R2, g.C2, g.C1, a.k_sb, a.k_sh, a.k_sr, a.smooth_k, a.fold);
   else
-    hipLaunchKernelGGL((k_quant_kernel<T, false, D>), dim3((unsigned)g.C2, (unsigned)BH), dim3(PT), 0,
+    hipLaunchKernelGGL((k_quant_kernel<T, false, D>), grid2, dim3(PT), 0,
                        stream, (const T*)a.k, (u8*)a.k8, a.sk, a.sv, part, smax, a.mean, a.s, a.kconst, a.H,
-                       a.N, a.N_pad, g.R2, g.C1, a.k_sb, a.k_sh, a.k_sr, a.smooth_k, a.fold);
+                       a.N, a.N_pad, g.R2, g.C2, g.C1, a.k_sb, a.k_sh, a.k_sr, a.smooth_k, a.fold);
   return hipGetLastError();
+}
+
+// MEAN from the stats pass's K partials: the reduction of k_quant_kernel (same order, same
+// rounding), one block of D threads per plane.
+template <int D>
+__global__ __launch_bounds__(D) void mean_reduce_kernel(const double* __restrict__ part,
+                                                        float* __restrict__ MEAN, int64_t N,
+                                                        int64_t C1) {
+  const int64_t bh = blockIdx.x;
+  const int tid = threadIdx.x;
+  double s = 0.0;
+  for (int64_t c = 0; c < C1; ++c) s += part[(bh * C1 + c) * D + tid];
+  MEAN[bh * D + tid] = (float)(s / (double)N);
+}
+
+template <typename T, int D>
+static hipError_t launch_kseq_mean_t(const PrologueArgs& a, hipStream_t stream) {
+  const int64_t BH = a.B * a.H;
+  const PrologueGeom g = prologue_geom(BH, a.N, a.N_pad, Geo<D>::STEP);
+  double* part = (double*)a.workspace;
+  hipLaunchKernelGGL((kv_stats_kernel<T, K_ONLY, D>), dim3((unsigned)(g.C1 * BH)), dim3(PT), 0,
+                     stream, (const T*)a.k, (const T*)a.k, nullptr, nullptr, part, nullptr, nullptr,
+                     nullptr, a.H, a.N, a.N_pad, g.R1, g.C1, a.k_sb, a.k_sh, a.k_sr, a.k_sb,
+                     a.k_sh, a.k_sr, 1);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((mean_reduce_kernel<D>), dim3((unsigned)BH), dim3(D), 0, stream, part, a.mean,
+                     a.N, g.C1);
+  return hipGetLastError();
+}
+
+hipError_t launch_kseq_mean(const PrologueArgs& a, hipStream_t stream) {
+  if (a.D == 64)
+    return a.dtype == 1 ? launch_kseq_mean_t<bf16, 64>(a, stream)
+                        : launch_kseq_mean_t<f16, 64>(a, stream);
+  return a.dtype == 1 ? launch_kseq_mean_t<bf16, 128>(a, stream)
+                      : launch_kseq_mean_t<f16, 128>(a, stream);
 }
 
 hipError_t launch_prologue(const PrologueArgs& a, hipStream_t stream) {

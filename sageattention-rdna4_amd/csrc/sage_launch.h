@@ -6,17 +6,20 @@
 
 namespace sage {
 
-// Geometry of the two-launch prologue for BH planes of N rows (N_pad = ceil(N/64)*64). The
-// workspace is sized for head_dim 128, which covers 64.
-//   stats pass: grid (C1, BH), each block owns R1 consecutive rows of one plane;
-//   quant pass: grid (ceil(N_pad/R2), BH), each block owns R2 rows.
+// Geometry of the two-launch prologue for BH planes of N rows, padded to N_pad (a multiple of 64,
+// at least ceil(N/64)*64). The workspace is sized for head_dim 128, which covers 64.
+//   stats pass: C1 blocks per plane (1-D grid of C1*BH), each owning R1 consecutive rows; R1 and
+//               C1 follow from Nc = ceil(N/64)*64, and the plane's last block also covers the
+//               rows up to N_pad, so extra padding never changes the workspace;
+//   quant pass: C2 blocks per plane (1-D grid of C2*BH), each owning R2 rows of N_pad.
 // Each grid is one round of resident blocks on MI355X (prologue.hip), so C1 stays small and the
 // quant blocks' reduction of the C1 mean partials (128 fp64 each) stays short.
 struct PrologueGeom {
   int64_t R1, C1, R2, C2;
 };
-PrologueGeom prologue_geom(int64_t BH, int64_t N_pad, int64_t step = 128);
-size_t prologue_workspace_bytes(int64_t BH, int64_t N_pad);
+PrologueGeom prologue_geom(int64_t BH, int64_t N, int64_t N_pad, int64_t step = 128);
+// bytes of workspace for BH planes of N rows (any N_pad)
+size_t prologue_workspace_bytes(int64_t BH, int64_t N);
 
 struct PrologueArgs {
   int dtype, k_int8, smooth_k, smooth_v, fold;
@@ -37,6 +40,9 @@ struct PrologueArgs {
   void* workspace;
 };
 hipError_t launch_prologue(const PrologueArgs& a, hipStream_t stream);
+// The smooth_k mean alone: K's fp64 column partials (stats pass, K only), then MEAN, with the
+// same summation order and rounding as the prologue's MEAN output.
+hipError_t launch_kseq_mean(const PrologueArgs& a, hipStream_t stream);
 
 struct AttnArgs {
   int dtype, qk_int8, causal;

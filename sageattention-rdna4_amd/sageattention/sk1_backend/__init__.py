@@ -34,7 +34,7 @@ ENVELOPE = dict(
     contiguous="any view strided_view_reason accepts",
     causal=(0, 1),
     smooth_k=(False, True),
-    batch_heads="B*H <= 65535",
+    batch_heads="any",
     heads="H_kv divides H (grouped-query / multi-query K/V heads)",
     seq_len="N >= 1, N_kv >= 1; N == N_kv when causal",
     return_lse=(False, True),
@@ -114,8 +114,6 @@ def _envelope_ok(q, k, v, tensor_layout, is_causal, sm_scale, return_lse, smooth
         return "seq_len"
     if is_causal and q.size(2) != k.size(2):
         return "seq_len"
-    if q.size(0) * q.size(1) > 65535:
-        return "batch_heads"
     return None
 
 

@@ -15,20 +15,17 @@ import collections
 
 import torch
 
-from .sk1_loader import SageLib, strided_view_reason
+from .sk1_loader import STRIDED_REFUSALS, SageLib, strided_view_reason
 
 HEAD_DIMS = (64, 128)
 BN = 64
 FLOOR = 1e-12
 
-#: every reason `check` / `quant_kv` can return, so a test can enumerate them
+#: every reason `check` / `quant_kv` / `kseq_mean` can return, so a test can enumerate them
 REFUSALS = ("not_cuda", "rank", "shape", "dtype_mismatch", "bf16_int8", "dtype", "head_dim",
             "device", "n_pad", "n_lt_1", "floor", "launch", "mean_dtype", "mean_head_dim",
             "mean_launch") + tuple(
-    "k_" + r for r in ("rank", "stride_last", "stride_nonpos", "stride_align", "ptr_align",
-                       "stride_overlap", "stride_int32")) + tuple(
-    "v_" + r for r in ("rank", "stride_last", "stride_nonpos", "stride_align", "ptr_align",
-                       "stride_overlap", "stride_int32"))
+    p + r for p in ("k_", "v_", "mean_") for r in STRIDED_REFUSALS)
 
 
 def n_pad_for(N: int) -> int:
@@ -135,7 +132,12 @@ class HipPrologue:
         return res
 
     def kseq_mean(self, k):
-        """The smooth_k sequence mean (B, H, D) fp32, or `None` if refused."""
+        """The smooth_k sequence mean (B, H, D) fp32, or `None` if refused (never raises).
+
+        fp64 sums of the exactly widened inputs in a fixed order, one fp32 rounding: the same bits
+        as the `mean` the prologue subtracts (`hip_prologue.py:267-292` of the reference, whose
+        kernel is `h34_kseq_mean_*`). K is read once; V is not read.
+        """
         if k.dim() != 4 or not k.is_cuda or k.dtype not in (torch.float16, torch.bfloat16):
             return self._refuse("mean_dtype")
         B, H, N, D = (int(x) for x in k.shape)
@@ -144,10 +146,19 @@ class HipPrologue:
         r = strided_view_reason(k, "k")
         if r is not None:
             return self._refuse("mean_" + r)
-        res = self.quant_kv(k, k, smooth_k=True, int8=(k.dtype == torch.float16), mean_out=True)
-        if res is None:
+        if N < 1:
+            return self._refuse("n_lt_1")
+        try:
+            mean = torch.empty(B * H, D, device=k.device, dtype=torch.float32)
+            ws = torch.empty(self.lib.workspace_bytes(B * H, N), device=k.device,
+                             dtype=torch.uint8)
+            with torch.cuda.device(k.device):
+                self.lib.kseq_mean(k, mean, ws)
+        except Exception as e:  # noqa: BLE001 - the reference's prologue contract is "never raises"
+            self.last_error = "%s: %s" % (type(e).__name__, e)
             return self._refuse("mean_launch")
-        return res[-1].view(B, H, D)
+        self.n_calls += 1
+        return mean.view(B, H, D)
 
     def _refuse(self, reason):
         self.n_refusals += 1

@@ -22,20 +22,23 @@ LIB_PATH = os.environ.get(
 SAGE_F16, SAGE_BF16 = 0, 1
 
 #: Every reason `strided_view_reason` can return, in evaluation order. The strings are the
-#: reference's refusal vocabulary (`sageattention/sk1_backend/sk1_loader.py:308-309`).
+#: reference's refusal vocabulary (`sageattention/sk1_backend/sk1_loader.py:308-309`); its
+#: `stride_int32` is not among them (see below).
 STRIDED_REFUSALS = ("rank", "stride_last", "stride_nonpos", "stride_align", "ptr_align",
-                    "stride_overlap", "stride_int32")
-_INT32_MAX = 2 ** 31 - 1
+                    "stride_overlap")
 
 
 def strided_view_reason(t, name="t"):
     """`None` if `t` is a servable logical (B, H, N, D) view, else the refusal reason.
 
-    The rule of the reference (`sageattention/sk1_backend/sk1_loader.py:313-369`), restated from the
-    needs of this build's kernels, which read Q/K/V and write O with 16-byte vector accesses:
-    rank 4; last stride 1; every stride positive and the outer three multiples of 8 elements; a
-    16-byte-aligned pointer; an injective index map (sizes-1 dims dropped, strides sorted, each at
-    least the previous stride times its size); strides within int32.
+    Derived from this build's kernels, which read Q/K/V and write O with 16-byte vector accesses
+    through int64 (batch, head, row) strides: rank 4; last stride 1 (the 16-byte accesses run
+    along D); every stride positive and the outer three multiples of 8 elements (each access
+    16-byte aligned); a 16-byte-aligned pointer; an injective index map, so that no two output
+    rows alias (sizes-1 dims dropped, strides sorted, each at least the previous stride times its
+    size). The reference's rule (`sageattention/sk1_backend/sk1_loader.py:313-369`) also refuses
+    strides beyond int32 (`stride_int32`), because its kernels take int strides; every address
+    here is formed in 64 bits, so no such refusal is needed.
     """
     if t.dim() != 4:
         return "rank"
@@ -52,8 +55,6 @@ def strided_view_reason(t, name="t"):
     for (s0, n0), (s1, _) in zip(dims, dims[1:]):
         if s1 < s0 * n0:
             return "stride_overlap"
-    if any(s > _INT32_MAX for s in st):
-        return "stride_int32"
     return None
 
 
@@ -126,6 +127,12 @@ class SageLib:
         L.sage_attn_fwd_ex.argtypes = ([i32] * 3 + [vp, i64, i64, i64] + [vp] * 4
                                        + [vp, i64, i64, i64] + [i64] * 7
                                        + [f32, i32, vp, vp, vp, vp])
+        L.sage_attn_fwd_sk.restype = i32
+        L.sage_attn_fwd_sk.argtypes = ([i32] * 3 + [vp, i64, i64, i64] + [vp] * 6
+                                       + [vp, i64, i64, i64] + [i64] * 7 + [f32, vp, vp, vp])
+        L.sage_kseq_mean.restype = i32
+        L.sage_kseq_mean.argtypes = [i32, vp, i64, i64, i64, i64, i64, i64, i64, vp, vp,
+                                     ctypes.c_size_t, vp]
         L.sage_quant_q.restype = i32
         L.sage_quant_q.argtypes = [i32, i32, vp, i64, i64, i64, i64, i64, i64, i64, f32, vp, vp,
                                    vp, vp]
@@ -186,6 +193,35 @@ class SageLib:
             B, H, N, bh_kv // B, n_kv, int(n_pad), D, ctypes.c_float(float(sm_scale)), int(kernel),
             _ptr(lse), _ptr(kmean), _ptr(vmean), ctypes.c_void_p(torch_stream(q.device)))
         self._check(rc, "sage_attn_fwd")
+
+    def attn_fwd_sk(self, q, k8, sk, v8t, sv, s, o, *, qk_int8, causal, sm_scale, n_kv=None,
+                    vmean=None, lse=None, kmean=None):
+        """Main loop on the reference kernel's inputs (see `sage_attn_fwd_sk`): `sk`, `sv`
+        (B*H_kv, n_pad) fp32 are SK and the folded SV'; `s` (B*H_kv,) the fold."""
+        B, H, N, D = (int(x) for x in q.shape)
+        bh_kv, n_pad = int(k8.shape[0]), int(k8.shape[1])
+        if bh_kv % B:
+            raise ValueError("sage_attn_fwd_sk: k8 holds %d planes, not a multiple of B=%d"
+                             % (bh_kv, B))
+        n_kv = N if n_kv is None else int(n_kv)
+        rc = self.lib.sage_attn_fwd_sk(
+            _dtype_code(q.dtype), int(bool(qk_int8)), int(bool(causal)),
+            _ptr(q), q.stride(0), q.stride(1), q.stride(2),
+            _ptr(k8), _ptr(sk), _ptr(v8t), _ptr(sv), _ptr(vmean), _ptr(s),
+            _ptr(o), o.stride(0), o.stride(1), o.stride(2),
+            B, H, N, bh_kv // B, n_kv, n_pad, D, ctypes.c_float(float(sm_scale)),
+            _ptr(lse), _ptr(kmean), ctypes.c_void_p(torch_stream(q.device)))
+        self._check(rc, "sage_attn_fwd_sk")
+
+    def kseq_mean(self, k, mean, workspace):
+        """The smooth_k mean of a logical (B, H, N, D) view into `mean` (B*H, D) fp32 (see
+        `sage_kseq_mean`)."""
+        B, H, N, D = (int(x) for x in k.shape)
+        rc = self.lib.sage_kseq_mean(
+            _dtype_code(k.dtype), _ptr(k), k.stride(0), k.stride(1), k.stride(2), B, H, N, D,
+            _ptr(mean), _ptr(workspace), int(workspace.numel() * workspace.element_size()),
+            ctypes.c_void_p(torch_stream(k.device)))
+        self._check(rc, "sage_kseq_mean")
 
     def quant_q(self, q, sm_scale, *, qk_int8):
         """Q quantized exactly as the main loop quantizes it: `(q8, sq, cq)` on q's device."""

@@ -22,8 +22,8 @@ def _declared_symbols():
 def test_header_declares_the_entry_points():
     syms = _declared_symbols()
     for s in ("sage_version", "sage_last_error", "sage_kv_prologue_workspace_bytes",
-              "sage_kv_prologue", "sage_attn_fwd", "sage_attn_fwd_ex", "sage_quant_q",
-              "sage_mfma_layout_probe"):
+              "sage_kv_prologue", "sage_attn_fwd", "sage_attn_fwd_ex", "sage_attn_fwd_sk",
+              "sage_kseq_mean", "sage_quant_q", "sage_mfma_layout_probe"):
         assert s in syms
 
 
@@ -83,6 +83,42 @@ def test_library_host_calls_without_a_gpu():
     rc = L.lib.sage_quant_q(0, 1, p16, 12800, 12800, 128, 1, 1, 100, 32, ctypes.c_float(0.1),
                             p16, p16, p16, None)
     assert rc == 1 and b"head_dim" in L.lib.sage_last_error()
+    # the workspace size depends on B*H and N only: a larger N_pad than ceil(N/64)*64 passes the
+    # size check with workspace_bytes(B*H, N) (the call then fails only at the launch, no GPU)
+    need = L.workspace_bytes(1, 64)
+    assert need == L.workspace_bytes(1, 33)
+    rc = L.lib.sage_kv_prologue(0, 1, 1, 0, 1, p16, 64 * 128, 64 * 128, 128, p16, 64 * 128,
+                                64 * 128, 128, 1, 1, 64, 256, 128, p16, p16, p16, p16, None,
+                                None, p16, None, ctypes.c_void_p(256), need, None)
+    assert b"workspace" not in L.lib.sage_last_error()
+    rc = L.lib.sage_kv_prologue(0, 1, 1, 0, 1, p16, 64 * 128, 64 * 128, 128, p16, 64 * 128,
+                                64 * 128, 128, 1, 1, 64, 256, 128, p16, p16, p16, p16, None,
+                                None, p16, None, ctypes.c_void_p(256), need - 8, None)
+    assert rc == 1 and b"workspace" in L.lib.sage_last_error()
+    # B*H beyond 65535 is a valid shape (the grids are 1-D); only the int32 block index bounds it
+    rc = L.lib.sage_attn_fwd(0, 1, 0, p16, 8, 8, 8, None, None, None, None, p16, 8, 8, 8,
+                             1, 70000, 100, 128, ctypes.c_float(0.1), None)
+    assert b"grid" not in L.lib.sage_last_error()
+    rc = L.lib.sage_attn_fwd(0, 1, 0, p16, 8, 8, 8, None, None, None, None, p16, 8, 8, 8,
+                             1 << 20, 1 << 12, 1 << 10, 1 << 10, ctypes.c_float(0.1), None)
+    assert rc == 1 and b"grid" in L.lib.sage_last_error()
+    # the main loop on SK / SV' and the mean alone refuse like the others
+    def sk(**kw):
+        a = dict(dtype=0, qk_int8=1, causal=0, D=128, H_kv=1, N_kv=100, sk=p16)
+        a.update(kw)
+        return L.lib.sage_attn_fwd_sk(a["dtype"], a["qk_int8"], a["causal"], p16, 12800, 12800,
+                                      128, p16, a["sk"], p16, p16, None, p16, p16, 12800, 12800,
+                                      128, 1, 1, 100, a["H_kv"], a["N_kv"], 128, a["D"],
+                                      ctypes.c_float(0.1), None, None, None)
+    assert sk(dtype=1) == 1 and b"bf16_int8" in L.lib.sage_last_error()
+    assert sk(D=96) == 1 and b"head_dim" in L.lib.sage_last_error()
+    assert sk(causal=1, N_kv=99) == 1 and b"seq_len" in L.lib.sage_last_error()
+    assert sk(sk=ctypes.c_void_p(20)) == 1 and b"ptr_align" in L.lib.sage_last_error()
+    assert sk(sk=None) == 1 and b"NULL" in L.lib.sage_last_error()
+    rc = L.lib.sage_kseq_mean(0, p16, 12800, 12800, 128, 1, 1, 100, 96, p16, p16, 1 << 20, None)
+    assert rc == 1 and b"mean_head_dim" in L.lib.sage_last_error()
+    rc = L.lib.sage_kseq_mean(0, p16, 12800, 12800, 128, 1, 1, 100, 128, p16, p16, 8, None)
+    assert rc == 1 and b"workspace" in L.lib.sage_last_error()
     # smooth_v needs somewhere to put V's mean
     rc = L.lib.sage_kv_prologue(0, 1, 1, 1, 1, p16, 12800, 12800, 128, p16, 12800, 12800, 128,
                                 1, 1, 100, 128, 128, p16, p16, p16, p16, None, None, p16, None,
@@ -119,6 +155,20 @@ def test_strided_view_reason_rule():
     qkv = torch.empty(100, 3 * 4 * 128, dtype=torch.float16)
     q = qkv.split(4 * 128, dim=-1)[1].view(100, 4, 128).transpose(0, 1).unsqueeze(0)
     assert r(q) is None
+    # strides beyond int32 are served (every address is formed in 64 bits): no stride_int32
+    big = torch.empty(1, dtype=torch.float16, device="meta").as_strided(
+        (2, 1, 4, 128), (2 ** 31 + 1024, 512, 128, 1))
+    assert r(big) is None
+
+
+def test_refusal_vocabularies():
+    from sageattention.sk1_backend.hip_prologue import REFUSALS
+    from sageattention.sk1_backend.sk1_loader import STRIDED_REFUSALS
+    assert "stride_int32" not in STRIDED_REFUSALS
+    for p in ("k_", "v_", "mean_"):
+        for r in STRIDED_REFUSALS:
+            assert p + r in REFUSALS
+    assert len(set(REFUSALS)) == len(REFUSALS)
 
 
 def test_envelope_reasons_on_cpu_tensors():
