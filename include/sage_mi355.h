@@ -107,6 +107,27 @@ int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int smooth_v, int fold
                      void* stream);
 
 /*
+ * `sage_kv_prologue` without the workspace arguments: the prologue's workspace (the fp64 mean
+ * partials and per-block V maxima) is a static device array of SAGE_NOALLOC_SCRATCH_BYTES that
+ * the library holds on each GPU it runs on until the process ends. No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Nothing is allocated by this call.
+ *
+ * Limit: a call whose `sage_kv_prologue_workspace_bytes(B*H, N)` exceeds
+ * SAGE_NOALLOC_SCRATCH_BYTES returns SAGE_ERR_INVALID ("scratch: ..."); that is every N for
+ * B*H <= 768 and B*H up to ~2000 beyond. Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (two streams, two host threads) race and must be serialized by the caller.
+ * Nothing in the array needs to start at zero (each call writes every partial it reads).
+ */
+#define SAGE_NOALLOC_SCRATCH_BYTES (4u << 20)
+int sage_kv_prologue_noalloc(int dtype, int k_int8, int smooth_k, int smooth_v, int fold,
+                             const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sr,
+                             const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sr,
+                             int64_t B, int64_t H, int64_t N, int64_t N_pad, int64_t D,
+                             void* k8, float* sk, void* v8t, float* sv, float* mean, float* vmean,
+                             float* s, float* kconst, void* stream);
+
+/*
  * The quantized flash-attention main loop (one launch on `stream`).
  *
  * Replaces `Sk1Attn.launch` / `Sk1Attn.launch_strided`

@@ -4,6 +4,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <string>
 
 #include "../../include/sage_mi355.h"
@@ -67,6 +68,41 @@ int check_shape(int64_t B, int64_t H, int64_t N, int64_t N_pad) {
 int check_head_dim(int64_t D) {
   if (D != 64 && D != 128)
     return fail(SAGE_ERR_INVALID, "head_dim: D must be 64 or 128 (got %lld)", (long long)D);
+  return SAGE_OK;
+}
+
+}  // namespace
+
+// The workspace of sage_kv_prologue_noalloc: one copy per GPU, loaded with the code object and held
+// until the process ends. Host code never passes `scratch` itself (on the host it names a
+// stand-in, not device memory): it passes the device address that hipGetSymbolAddress returns for
+// the current device, kept in g_scratch_ptr.
+static __device__ __align__(256) unsigned char scratch[SAGE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device with that device current.
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "sage_kv_prologue_noalloc hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(SAGE_ERR_INVALID, "scratch: device %d beyond the %d the library tracks", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, "sage_kv_prologue_noalloc hipGetSymbolAddress");
+    if (p == nullptr || ((uintptr_t)p & 255u))
+      return fail(SAGE_ERR_HIP, "scratch: hipGetSymbolAddress gave an unusable address %p", p);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
   return SAGE_OK;
 }
 
@@ -137,6 +173,27 @@ int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int smooth_v, int fold
   a.kconst = kconst;
   a.workspace = workspace;
   return hip_status(sage::launch_prologue(a, (hipStream_t)stream), "sage_kv_prologue launch");
+}
+
+int sage_kv_prologue_noalloc(int dtype, int k_int8, int smooth_k, int smooth_v, int fold,
+                             const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sr,
+                             const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sr, int64_t B,
+                             int64_t H, int64_t N, int64_t N_pad, int64_t D, void* k8, float* sk,
+                             void* v8t, float* sv, float* mean, float* vmean, float* s,
+                             float* kconst, void* stream) {
+  int rc = check_shape(B, H, N, N_pad);
+  if (rc) return rc;
+  const size_t need = sage::prologue_workspace_bytes(B * H, N);
+  if (need > (size_t)SAGE_NOALLOC_SCRATCH_BYTES)
+    return fail(SAGE_ERR_INVALID,
+                "scratch: B*H=%lld N=%lld needs a %zu-byte workspace, the static scratch holds %zu "
+                "(use sage_kv_prologue with a workspace of that size)",
+                (long long)(B * H), (long long)N, need, (size_t)SAGE_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if ((rc = scratch_for_current_device(&ws))) return rc;
+  return sage_kv_prologue(dtype, k_int8, smooth_k, smooth_v, fold, k, k_sb, k_sh, k_sr, v, v_sb,
+                          v_sh, v_sr, B, H, N, N_pad, D, k8, sk, v8t, sv, mean, vmean, s, kconst,
+                          ws, (size_t)SAGE_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t q_sb,

@@ -120,6 +120,9 @@ class SageLib:
         L.sage_kv_prologue.restype = i32
         L.sage_kv_prologue.argtypes = ([i32] * 5 + [vp, i64, i64, i64] * 2 + [i64] * 5
                                        + [vp] * 9 + [ctypes.c_size_t, vp])
+        L.sage_kv_prologue_noalloc.restype = i32
+        L.sage_kv_prologue_noalloc.argtypes = ([i32] * 5 + [vp, i64, i64, i64] * 2 + [i64] * 5
+                                               + [vp] * 9)
         L.sage_attn_fwd.restype = i32
         L.sage_attn_fwd.argtypes = ([i32] * 3 + [vp, i64, i64, i64] + [vp] * 4
                                     + [vp, i64, i64, i64] + [i64] * 4 + [f32, vp])
@@ -171,6 +174,19 @@ class SageLib:
             int(workspace.numel() * workspace.element_size()),
             ctypes.c_void_p(torch_stream(k.device)))
         self._check(rc, "sage_kv_prologue")
+
+    def kv_prologue_noalloc(self, k, v, k8, sk, v8t, sv, s, mean, *, k_int8, smooth_k, fold,
+                            n_pad, kconst=None, smooth_v=False, vmean=None):
+        """`kv_prologue` with the library's static per-GPU scratch as its workspace (see
+        `sage_kv_prologue_noalloc`): nothing is allocated. Calls overlapping on one GPU race."""
+        B, H, N, D = (int(x) for x in k.shape)
+        rc = self.lib.sage_kv_prologue_noalloc(
+            _dtype_code(k.dtype), int(bool(k_int8)), int(bool(smooth_k)), int(bool(smooth_v)),
+            int(bool(fold)), _ptr(k), k.stride(0), k.stride(1), k.stride(2),
+            _ptr(v), v.stride(0), v.stride(1), v.stride(2),
+            B, H, N, int(n_pad), D, _ptr(k8), _ptr(sk), _ptr(v8t), _ptr(sv), _ptr(mean),
+            _ptr(vmean), _ptr(s), _ptr(kconst), ctypes.c_void_p(torch_stream(k.device)))
+        self._check(rc, "sage_kv_prologue_noalloc")
 
     def attn_fwd(self, q, k8, kconst, v8t, s, o, *, qk_int8, causal, sm_scale, n_pad, kernel=0,
                  lse=None, kmean=None, n_kv=None, vmean=None):
