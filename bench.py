@@ -7,11 +7,27 @@ inputs already resident in HBM. The default workload is BASELINE's headline, con
 B=1, H=48, N=47520, D=128, causal, smooth_k on, HND. Ops convention 4*B*H*N^2*D, halved when
 causal (the reference's `bench/bench_attention.py:140`).
 
+The method follows the reference's (`docs/METHOD.md:14-45`, `bench/bench_attention.py:49-58`):
+1. W untimed warm-up calls, then an untimed clock-settling phase by time: at least `--settle`
+   seconds (default 4) and 40 calls, continued in half-second chunks while the shader clock still
+   rises (at most 10 s). Recorded as `settle` (calls, seconds, the clock readings).
+2. The timed region: exactly K calls of the public `sageattn(...)` (with `--kernel` other than 0,
+   of `sk1_forward` with that kernel), bracketed by device synchronizations, with the shader
+   clock read before and after. `ms_per_step` and `value` come from it.
+3. An A/A twin: the same call timed as two candidates over 10 interleaved rounds (order rotated
+   each round, one HIP event pair per batch of calls); `aa_ratio` = median B / median A, whose
+   distance from 1 is the noise floor of this run.
+4. The prologue/main-loop split: K calls of `sk1_forward` with HIP events on the launch stream
+   between its launches.
+5. The MFMA ceiling at this run's clock: the library's register-resident probe
+   (`sage_mfma_peak_probe`, int8 and e4m3), reported as `measured_peak` beside the documented
+   5.0 POPS.
+
 Prints ONE JSON line. Besides the contract fields it carries
 * `roofline`: the main-loop kernel's achieved TFLOP/s (algorithmic ops per launch / its mean
-  launch duration, timed with HIP events on the launch stream inside the timed region) against
-  the int8/fp8 dense MFMA peak; `traffic` is its HBM bytes per launch from the committed
-  rocprofv3 FETCH_SIZE/WRITE_SIZE summary for the workload (null when none is committed);
+  launch duration from step 4) against the int8/fp8 dense MFMA peak, and against the measured
+  one (`frac_of_measured`); `traffic` is its HBM bytes per launch from the committed rocprofv3
+  FETCH_SIZE/WRITE_SIZE summary for the workload (null when none is committed);
 * `prologue`: the prologue pair's achieved HBM GB/s on its algorithmic bytes;
 * `cpu_baseline`: the CPU emulation of the reference scheme (`oracle/`, a "port") and torch CPU
   SDPA, timed on a bounded sample of the same workload on this host's cores.
@@ -28,6 +44,9 @@ sys.path.insert(0, os.path.join(ROOT, "sageattention-rdna4_amd"))
 METRIC = "effective TOPS (full call incl. quant) fp16 B1 H48 D128 N47520 causal; % MFMA peak"
 PEAK_TOPS = 5000.0          # MI355X dense int8 (5.0 POPS) and fp8 (5.0 PFLOP/s) MFMA peak
 HBM_PEAK_GBPS = 8000.0
+# s_memrealtime's rate on MI355X (hipDeviceAttributeWallClockRate reads 100000 kHz; a probe's
+# tick span over its event-timed launch measured 99.8-99.96 MHz)
+REALTIME_MHZ = 100.0
 
 WORKLOADS = {
     # name: (dtype, B, H, N, causal, layout, k_offset_std, outlier_frac, std[, head_dim])
@@ -182,6 +201,87 @@ def sclk_mhz():
     return None
 
 
+def settle(call, sync, *, min_calls=40, min_s=4.0, max_s=10.0, chunk_s=0.5, max_calls=20000,
+           clock=None, now=time.perf_counter):
+    """Untimed clock settling by time, not by call count (the reference's rule,
+    `docs/METHOD.md:23-25`): calls (each followed by `sync`) until at least `min_calls` calls and
+    `min_s` seconds have passed, then on in `chunk_s` chunks while the shader clock reading still
+    rises, until `max_s`; `max_calls` caps the count so a call that returns at once cannot spin
+    forever. Returns the calls made, the seconds spent and the clock readings (MHz, None where
+    unreadable) at the start, after the floor and after each chunk."""
+    clock = clock or sclk_mhz
+    t0 = now()
+    trace = [clock()]
+    n = 0
+    while (n < min_calls or now() - t0 < min_s) and n < max_calls:
+        call()
+        sync()
+        n += 1
+    trace.append(clock())
+    while now() - t0 < max_s and n < max_calls:
+        t1 = now()
+        while now() - t1 < chunk_s and n < max_calls:
+            call()
+            sync()
+            n += 1
+        trace.append(clock())
+        if trace[-2] is None or trace[-1] is None or trace[-1] <= trace[-2]:
+            break
+    return {"calls": n, "seconds": round(now() - t0, 3), "sclk_mhz": trace}
+
+
+def aa_twin(call, make_event, sync, *, rounds=10, batch=5):
+    """The A/A twin (`docs/METHOD.md:14-22`): the same call measured as two candidates, A and B,
+    over `rounds` interleaved rounds with the order swapped every round; each measurement is one
+    event pair around a batch of `batch` calls. Returns both medians (ms per call) and their
+    ratio B/A, whose distance from 1 is the run's noise floor."""
+    import statistics
+    res = {"A": [], "B": []}
+    for r in range(rounds):
+        for name in (("A", "B") if r % 2 == 0 else ("B", "A")):
+            e0, e1 = make_event(), make_event()
+            e0.record()
+            for _ in range(batch):
+                call()
+            e1.record()
+            sync()
+            res[name].append(e0.elapsed_time(e1) / batch)
+    ma, mb = statistics.median(res["A"]), statistics.median(res["B"])
+    return {"rounds": rounds, "batch": batch, "ms_a": round(ma, 4), "ms_b": round(mb, 4),
+            "ratio": round(mb / ma, 4)}
+
+
+def mfma_peak(lib, qk_int8, make_event, sync, *, target_ms=25.0, reps=5):
+    """The dense MFMA rate at this run's clock, from the library's register-resident probe: one
+    short launch sizes the iteration count to about `target_ms` per launch, then `reps` launches
+    are timed with event pairs. Returns TOPS of the median launch and the shader clock (MHz) its
+    first wave ran at."""
+    import statistics
+    import torch
+    blocks = 4 * torch.cuda.get_device_properties(0).multi_processor_count
+
+    clocks = torch.zeros(2, dtype=torch.int64, device="cuda:0")
+
+    def timed(iters):
+        e0, e1 = make_event(), make_event()
+        e0.record()
+        ops = lib.mfma_peak_probe(qk_int8, blocks, iters, clocks)
+        e1.record()
+        sync()
+        cyc, ticks = (int(x) for x in clocks.cpu())
+        return ops, e0.elapsed_time(e1), cyc, ticks
+
+    timed(2000)                  # the first launch also pays its code object's first use
+    _, ms, _, _ = timed(2000)
+    iters = max(2000, int(2000 * target_ms / max(ms, 1e-3)))
+    runs = sorted((timed(iters) for _ in range(reps)), key=lambda r: r[1])
+    ops, ms, cyc, ticks = runs[len(runs) // 2]
+    # the first wave's shader-clock cycles over its constant-rate ticks (s_memrealtime counts at
+    # REALTIME_MHZ) give the clock the matrix cores ran at
+    mhz = cyc / ticks * REALTIME_MHZ if ticks else None
+    return ops / (ms * 1e-3) / 1e12, mhz
+
+
 def copy_calibration(mib, reps):
     """A plain device-to-device copy of `mib` MiB, `reps` times: each launch reads and writes
     exactly mib MiB, which calibrates what the HBM counters report per algorithmic byte."""
@@ -201,9 +301,16 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    # about a second of calls at the headline: the shader clock ramps up over the first calls
-    # (measured 1836 MHz before a 2-call warm-up's timed region, 2277 MHz after it)
     ap.add_argument("--warmup", type=int, default=50)
+    # the shader clock ramps up over the first seconds of calls (measured 1819 MHz at the start of
+    # a timed region after a 5-call warm-up, 2212 MHz at its end): settle by time as well
+    ap.add_argument("--settle", type=float, default=4.0,
+                    help="seconds of untimed calls after the warm-up (at least; see settle()); "
+                         "0 skips the phase (counter-collection runs)")
+    ap.add_argument("--aa-rounds", type=int, default=10,
+                    help="rounds of the A/A twin (0 skips it: counter-collection runs)")
+    ap.add_argument("--no-peak", action="store_true",
+                    help="skip the MFMA ceiling probe (counter-collection runs)")
     ap.add_argument("--workload", default="c3c", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
@@ -222,7 +329,7 @@ def main():
     import torch
     if args.copy_mib:
         return copy_calibration(args.copy_mib, max(args.steps, 1))
-    from sageattention import sageattn  # noqa: F401
+    from sageattention import sageattn
     from sageattention.sk1_backend import SageLib, sk1_forward
 
     wl = WORKLOADS[args.workload]
@@ -232,40 +339,84 @@ def main():
     dev = torch.device("cuda:0")
     qd, kd, vd = (t.to(dev) for t in (q, k, v))
     lib = SageLib.get()
-    call = lambda ev=None: sk1_forward(lib, qd, kd, vd, tensor_layout=layout, is_causal=causal,
-                                       smooth_k=True, events=ev, kernel=args.kernel)
+    split_call = lambda ev=None: sk1_forward(lib, qd, kd, vd, tensor_layout=layout,
+                                             is_causal=causal, smooth_k=True, events=ev,
+                                             kernel=args.kernel)
+    if args.kernel == 0:
+        call = lambda: sageattn(qd, kd, vd, tensor_layout=layout, is_causal=causal, smooth_k=True)
+        timed_call = "sageattn"
+    else:
+        call = split_call
+        timed_call = "sk1_forward(kernel=%d)" % args.kernel
     # the library's choice by size (sage_attn_fwd_ex): 256 queries per block from N = 32768 on,
     # head_dim 128 only
     q256 = args.kernel == 2 or (args.kernel == 0 and N >= 32768 and D == 128)
     kname = ("attn_fwd_pl_kernel" if args.kernel == 3 else
              "attn_fwd_pp_kernel" if q256 else "attn_fwd_kernel")
+    sync = torch.cuda.synchronize
+    event = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     for _ in range(args.warmup):
         call()
-    torch.cuda.synchronize()
+    sync()
+    st = settle(call, sync, min_s=args.settle) if args.settle > 0 else None
+    log("settle:", st)
 
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
+    # the timed region: exactly K calls
+    sync()
     clk0 = sclk_mhz()
-    torch.cuda.synchronize()
+    e0, e1 = event(), event()
+    sync()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        call(evs[i])
-    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(args.steps):
+        call()
+    e1.record()
+    sync()
     wall = time.perf_counter() - t0
     clk1 = sclk_mhz()
     ms_step = wall * 1e3 / args.steps
+    ev_ms = e0.elapsed_time(e1) / args.steps
+
+    aa = (aa_twin(call, event, sync, rounds=args.aa_rounds,
+                  batch=max(1, min(10, int(100.0 / max(ms_step, 1e-3)))))
+          if args.aa_rounds > 0 else None)
+    log("A/A twin:", aa)
+
+    # the prologue / main-loop split, from events between sk1_forward's launches
+    evs = [[event() for _ in range(3)] for _ in range(args.steps)]
+    sync()
+    for i in range(args.steps):
+        split_call(evs[i])
+    sync()
     steps_ms = sorted(e[0].elapsed_time(e[2]) for e in evs)
     pro_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
     attn_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
-    ev_ms = sum(e[0].elapsed_time(e[2]) for e in evs) / args.steps
+    split_ms = sum(e[0].elapsed_time(e[2]) for e in evs) / args.steps
+
+    peak, measured = None, None
+    if not args.no_peak:
+        clk_p0 = sclk_mhz()
+        i8_tops, i8_mhz = mfma_peak(lib, True, event, sync)
+        f8_tops, f8_mhz = mfma_peak(lib, False, event, sync)
+        peak = {"int8_tops": round(i8_tops, 1), "fp8_tops": round(f8_tops, 1),
+                "int8_run_mhz": None if i8_mhz is None else round(i8_mhz),
+                "fp8_run_mhz": None if f8_mhz is None else round(f8_mhz),
+                "documented_tops": PEAK_TOPS,
+                "sclk_mhz": {"before": clk_p0, "after": sclk_mhz()},
+                "probe": "sage_mfma_peak_probe: %d blocks x 4 waves, 4 independent "
+                         "register-resident MFMAs per wave per round"
+                         % (4 * torch.cuda.get_device_properties(0).multi_processor_count)}
+        log("measured MFMA peak:", peak)
+        measured = peak["int8_tops"] if dt == "fp16" else peak["fp8_tops"]
 
     ops = ops_of(B, H, N, causal, D)
     value = ops / (ms_step * 1e-3) / 1e12
     attn_tflops = ops / (attn_ms * 1e-3) / 1e12
     pbytes = prologue_bytes(B, H, N, D=D)
     pro_gbps = pbytes / (pro_ms * 1e-3) / 1e9
-    log("workload %s: %.3f ms/step (events %.3f), prologue %.3f ms (%.0f GB/s), main loop %.3f ms"
-        " (%.1f TFLOP/s)" % (args.workload, ms_step, ev_ms, pro_ms, pro_gbps, attn_ms, attn_tflops))
+    log("workload %s: %.3f ms/step (events %.3f), split: prologue %.3f ms (%.0f GB/s), main loop"
+        " %.3f ms (%.1f TFLOP/s)" % (args.workload, ms_step, ev_ms, pro_ms, pro_gbps, attn_ms,
+                                     attn_tflops))
 
     cpu = None
     if not args.no_cpu:
@@ -290,18 +441,27 @@ def main():
         "config": {"workload": "%s: %s B=%d H=%d N=%d D=%d %s smooth_k %s" % (
             args.workload, dt, B, H, N, D, "causal" if causal else "non-causal", layout),
             "global_batch": B, "seq_len": N, "parallelism": "single-gpu"},
+        "timed_call": timed_call,
+        "settle": st,
+        "aa_ratio": None if aa is None else aa["ratio"],
+        "aa_twin": aa,
+        "measured_peak": peak,
         "roofline": {"bound": "mfma", "achieved": round(attn_tflops, 1), "peak": PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(attn_tflops / PEAK_TOPS, 4),
+                     "frac_of_measured": (None if measured is None
+                                          else round(attn_tflops / measured, 4)),
                      "traffic": profiled_traffic(args.workload), "kernel": kname,
                      "ms": round(attn_ms, 4)},
         "prologue": {"ms": round(pro_ms, 4), "bytes": pbytes, "achieved_GBps": round(pro_gbps, 1),
                      "peak_GBps": HBM_PEAK_GBPS, "frac": round(pro_gbps / HBM_PEAK_GBPS, 4)},
         "cpu_baseline": cpu,
-        # per-step full-call times from the HIP events (the same steps as ms_per_step) and the
+        # the timed region's HIP-event time per call, the split pass's per-call times, and the
         # shader clock before and after the timed region: box-to-box clock differences are the
         # largest source of spread between runs
-        "step_ms": {"min": round(steps_ms[0], 4), "median": round(steps_ms[len(steps_ms) // 2], 4),
-                    "max": round(steps_ms[-1], 4)},
+        "event_ms_per_step": round(ev_ms, 4),
+        "split_step_ms": {"mean": round(split_ms, 4), "min": round(steps_ms[0], 4),
+                          "median": round(steps_ms[len(steps_ms) // 2], 4),
+                          "max": round(steps_ms[-1], 4)},
         "sclk_mhz": {"before": clk0, "after": clk1},
     }
     print(json.dumps(res), flush=True)

@@ -233,6 +233,21 @@ int sage_quant_q(int dtype, int qk_int8,
 int sage_mfma_layout_probe(const void* a, const void* bt, int32_t* c,
                            const void* e, const void* ft, float* d, void* stream);
 
+/*
+ * Benchmark probe, not on the served path: the dense rate of the main loop's matrix instructions
+ * on this GPU at the clock it runs at (the reference reports its register-resident ceiling beside
+ * the documented peak, `docs/METHOD.md:80-91`; no kernel of the reference's library does this).
+ * Launches `blocks` blocks of 4 waves; each wave issues `iters` rounds of 4 independent
+ * register-resident MFMAs: v_mfma_i32_32x32x32_i8 (qk_int8 != 0) or the e4m3
+ * v_mfma_scale_f32_32x32x64_f8f6f4 with unit scales. Ops per launch:
+ * blocks * 4 * iters * 4 * 2*32*32*K, K = 32 (int8) or 64 (e4m3). Nothing is read from memory.
+ * `clocks` (optional, 2 int64 on the device): the first wave's shader-clock cycles (s_memtime) and
+ * constant-rate ticks (s_memrealtime) over its run, i.e. the clock the matrix cores ran at.
+ * blocks in [1, 2^20], iters in [1, 2^30].
+ */
+int sage_mfma_peak_probe(int qk_int8, int64_t blocks, int64_t iters, int64_t* clocks,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

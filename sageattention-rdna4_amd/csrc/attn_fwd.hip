@@ -309,6 +309,73 @@ __global__ __launch_bounds__(64) void layout_probe_kernel(const u8* __restrict__
 }
 
 // ---------------------------------------------------------------------------------------------
+// MFMA throughput probe (benchmark only): the dense rate of the two matrix instructions the main
+// loop issues, measured on this GPU at the clock it runs at. Every wave issues `iters` rounds of
+// PEAK_NACC independent register-resident MFMAs (int8 32x32x32, or e4m3 32x32x64 with unit
+// scales) on operands that are neither zero nor equal across lanes, so the matrix core's data
+// paths toggle as on real data. Nothing is loaded: an asm statement that takes the accumulators
+// in place (in AGPRs), after 64 wait states, keeps them live without any instruction reading
+// them, and no wave ends with an MFMA in flight. With `clocks`, the first wave stores the
+// shader-clock cycles (s_memtime) and constant-rate ticks (s_memrealtime) it spent.
+// Ops per launch: blocks * 4 waves * iters * PEAK_NACC * 2*32*32*K (K = 32 int8, 64 e4m3).
+// ---------------------------------------------------------------------------------------------
+constexpr int PEAK_NACC = 4;
+
+template <bool INT8>
+__global__ __launch_bounds__(256) void mfma_peak_kernel(int64_t iters, int64_t* __restrict__ clocks) {
+  const unsigned lane = threadIdx.x & 63;
+  const uint64_t c0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  if constexpr (INT8) {
+    i32x4 a, b;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[i] = (int)(0x9E3779B9u * (4 * lane + i + 1));
+      b[i] = (int)(0x85EBCA6Bu * (4 * lane + i + 7));
+    }
+    i32x16 acc[PEAK_NACC];
+#pragma unroll
+    for (int t = 0; t < PEAK_NACC; ++t)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[t][i] = 0;
+    int64_t it = iters;   // >= 1 (the entry point checks)
+    do {
+#pragma unroll
+      for (int t = 0; t < PEAK_NACC; ++t)
+        acc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[t], 0, 0, 0);
+    } while (--it > 0);
+    // 64 wait states, then the results are taken in place by an empty statement (no read)
+    asm volatile("s_nop 15\n s_nop 15\n s_nop 15\n s_nop 15"
+                 : "+a"(acc[0]), "+a"(acc[1]), "+a"(acc[2]), "+a"(acc[3]));
+  } else {
+    // bytes masked with 0x57: e4m3 values with exponent field <= 10 -- finite, never NaN
+    i32x8 a, b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a[i] = (int)((0x9E3779B9u * (8 * lane + i + 1)) & 0x57575757u);
+      b[i] = (int)((0x85EBCA6Bu * (8 * lane + i + 7)) & 0x57575757u);
+    }
+    f32x16 acc[PEAK_NACC];
+#pragma unroll
+    for (int t = 0; t < PEAK_NACC; ++t)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+    int64_t it = iters;
+    do {
+#pragma unroll
+      for (int t = 0; t < PEAK_NACC; ++t) acc[t] = mfma_f8(a, b, acc[t]);
+    } while (--it > 0);
+    asm volatile("s_nop 15\n s_nop 15\n s_nop 15\n s_nop 15"
+                 : "+a"(acc[0]), "+a"(acc[1]), "+a"(acc[2]), "+a"(acc[3]));
+  }
+  // the shader-clock cycles and constant-rate ticks the first wave spent: the clock it ran at
+  const uint64_t c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  if (clocks != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+    clocks[0] = (int64_t)(c1 - c0);
+    clocks[1] = (int64_t)(r1 - r0);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 template <typename T, bool QK_INT8, bool CAUSAL, int D>
 static void launch_attn_d(const AttnArgs& a, hipStream_t stream) {
   const int BH = (int)(a.B * a.H);
@@ -381,6 +448,17 @@ hipError_t launch_layout_probe(const void* a, const void* bt, int32_t* c, const 
                                const void* ft, float* d, hipStream_t stream) {
   hipLaunchKernelGGL(layout_probe_kernel, dim3(1), dim3(64), 0, stream, (const u8*)a,
                      (const u8*)bt, c, (const u8*)e, (const u8*)ft, d);
+  return hipGetLastError();
+}
+
+hipError_t launch_mfma_peak(bool int8, int64_t blocks, int64_t iters, int64_t* clocks,
+                            hipStream_t stream) {
+  if (int8)
+    hipLaunchKernelGGL(mfma_peak_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, iters,
+                       clocks);
+  else
+    hipLaunchKernelGGL(mfma_peak_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, iters,
+                       clocks);
   return hipGetLastError();
 }
 

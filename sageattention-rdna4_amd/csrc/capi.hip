@@ -426,4 +426,16 @@ int sage_mfma_layout_probe(const void* a, const void* bt, int32_t* c, const void
                     "sage_mfma_layout_probe launch");
 }
 
+int sage_mfma_peak_probe(int qk_int8, int64_t blocks, int64_t iters, int64_t* clocks,
+                         void* stream) {
+  if (blocks < 1 || blocks > (1 << 20))
+    return fail(SAGE_ERR_INVALID, "blocks must be in [1, 2^20] (got %lld)", (long long)blocks);
+  if (iters < 1 || iters > (1LL << 30))
+    return fail(SAGE_ERR_INVALID, "iters must be in [1, 2^30] (got %lld)", (long long)iters);
+  if (clocks != nullptr && ((uintptr_t)clocks & 7u))
+    return fail(SAGE_ERR_INVALID, "clocks must be 8-byte aligned");
+  return hip_status(sage::launch_mfma_peak(qk_int8 != 0, blocks, iters, clocks, (hipStream_t)stream),
+                    "sage_mfma_peak_probe launch");
+}
+
 }  // extern "C"

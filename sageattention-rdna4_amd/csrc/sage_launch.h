@@ -85,5 +85,8 @@ hipError_t launch_quant_q(const QuantQArgs& a, hipStream_t stream);
 
 hipError_t launch_layout_probe(const void* a, const void* bt, int32_t* c, const void* e,
                                const void* ft, float* d, hipStream_t stream);
+// MFMA throughput probe: blocks x 256 threads, each wave `iters` rounds of 4 independent MFMAs.
+hipError_t launch_mfma_peak(bool int8, int64_t blocks, int64_t iters, int64_t* clocks,
+                            hipStream_t stream);
 
 }  // namespace sage

@@ -141,6 +141,8 @@ class SageLib:
                                    vp, vp]
         L.sage_mfma_layout_probe.restype = i32
         L.sage_mfma_layout_probe.argtypes = [vp] * 7
+        L.sage_mfma_peak_probe.restype = i32
+        L.sage_mfma_peak_probe.argtypes = [i32, i64, i64, vp, vp]
         self.version = int(L.sage_version())
         images = hip_runtime_images()
         self.hip_runtime = images
@@ -253,6 +255,19 @@ class SageLib:
             ctypes.c_void_p(torch_stream(dev)))
         self._check(rc, "sage_quant_q")
         return q8, sq, cq
+
+    #: MFMAs per wave per round of `sage_mfma_peak_probe`, and waves per block
+    PEAK_NACC, PEAK_WAVES = 4, 4
+
+    def mfma_peak_probe(self, qk_int8, blocks, iters, clocks=None, device=None):
+        """Launch the MFMA throughput probe on the current stream of `device`; returns its op
+        count (see `sage_mfma_peak_probe`). `clocks` (optional, 2 int64 on the device) receives
+        the first wave's shader-clock cycles and constant-rate ticks."""
+        rc = self.lib.sage_mfma_peak_probe(int(bool(qk_int8)), int(blocks), int(iters),
+                                           _ptr(clocks), ctypes.c_void_p(torch_stream(device)))
+        self._check(rc, "sage_mfma_peak_probe")
+        k = 32 if qk_int8 else 64
+        return int(blocks) * self.PEAK_WAVES * int(iters) * self.PEAK_NACC * 2 * 32 * 32 * k
 
     def layout_probe(self, a, bt, e, ft):
         dev = a.device

@@ -62,3 +62,92 @@ def test_more_than_one_gpu_is_refused():
                          capture_output=True, text=True, timeout=120)
     assert res.returncode == 2
     assert "one GPU" in res.stderr and res.stdout == ""
+
+
+class _FakeClock:
+    """A fake host clock that advances by `dt` seconds per call made, and a shader clock that
+    rises by `step` MHz per reading until `top`."""
+
+    def __init__(self, dt, mhz0=1800, step=100, top=2200):
+        self.t, self.dt, self.calls = 0.0, dt, 0
+        self.mhz, self.step, self.top = mhz0, step, top
+
+    def call(self):
+        self.calls += 1
+        self.t += self.dt
+
+    def now(self):
+        return self.t
+
+    def sclk(self):
+        m = self.mhz
+        self.mhz = min(self.top, self.mhz + self.step)
+        return m
+
+
+def test_settle_floor_is_time_and_calls(bench):
+    # fast calls: the 4 s floor, not the call count, ends the floor phase
+    fc = _FakeClock(dt=0.001, step=0)
+    st = bench.settle(fc.call, lambda: None, min_calls=40, min_s=4.0, max_s=10.0,
+                      clock=fc.sclk, now=fc.now)
+    assert st["seconds"] >= 4.0 and st["calls"] >= 4000
+    # the clock stopped rising at once: one half-second chunk after the floor, then stop
+    assert st["seconds"] < 4.6
+    # slow calls: the 40-call floor, not the time, ends it
+    fc = _FakeClock(dt=0.5, step=0)
+    st = bench.settle(fc.call, lambda: None, min_calls=40, min_s=4.0, max_s=10.0,
+                      clock=fc.sclk, now=fc.now)
+    assert st["calls"] >= 40 and st["seconds"] >= 20.0
+
+
+def test_settle_continues_while_the_clock_rises(bench):
+    fc = _FakeClock(dt=0.01, mhz0=1800, step=50, top=2100)
+    st = bench.settle(fc.call, lambda: None, min_calls=40, min_s=2.0, max_s=10.0,
+                      clock=fc.sclk, now=fc.now)
+    # readings 1800 (start), 1850 (after the floor), then one per chunk while rising: 1900 ..
+    # 2100 (5 chunks), then 2100 again (not above, a 6th chunk) ends it
+    assert st["sclk_mhz"] == [1800, 1850, 1900, 1950, 2000, 2050, 2100, 2100]
+    assert 2.0 + 6 * 0.5 <= st["seconds"] <= 2.0 + 6 * 0.5 + 7 * 0.01  # one call over per phase
+    # bounded by max_s and by max_calls however the clock behaves
+    fc = _FakeClock(dt=0.01, step=10, top=10 ** 9)
+    st = bench.settle(fc.call, lambda: None, min_calls=40, min_s=2.0, max_s=3.0,
+                      clock=fc.sclk, now=fc.now)
+    assert st["seconds"] <= 3.0 + 0.5 + 0.02
+    fc = _FakeClock(dt=0.0, step=0)
+    st = bench.settle(fc.call, lambda: None, min_calls=40, min_s=2.0, max_s=3.0,
+                      clock=fc.sclk, now=fc.now, max_calls=500)
+    assert st["calls"] == 500
+    # an unreadable clock: the floor only, plus one chunk
+    fc = _FakeClock(dt=0.01)
+    st = bench.settle(fc.call, lambda: None, min_s=2.0, clock=lambda: None, now=fc.now)
+    assert st["sclk_mhz"][0] is None and st["seconds"] <= 2.0 + 0.5 + 0.02
+
+
+class _FakeEvent:
+    """Events on a fake device clock: each call takes `cost(i)` ms, recorded when it is made."""
+    device_ms = 0.0
+
+    def record(self):
+        self.t = _FakeEvent.device_ms
+
+    def elapsed_time(self, other):
+        return other.t - self.t
+
+
+def test_aa_twin_interleaves_and_reports_medians(bench):
+    order = []
+    state = {"n": 0}
+
+    def call():
+        # a clock ramp: every call 1 % cheaper than the one before
+        _FakeEvent.device_ms += 10.0 * (0.99 ** state["n"])
+        state["n"] += 1
+        order.append(state["n"])
+
+    _FakeEvent.device_ms = 0.0
+    aa = bench.aa_twin(call, _FakeEvent, lambda: None, rounds=10, batch=3)
+    assert aa["rounds"] == 10 and aa["batch"] == 3 and state["n"] == 60
+    # interleaving with the order swapped each round keeps the ratio near 1 under the ramp
+    # (a sequential A-then-B would report B ~25 % faster)
+    assert abs(aa["ratio"] - 1.0) < 0.05
+    assert 5.0 < aa["ms_a"] < 10.0 and 5.0 < aa["ms_b"] < 10.0

@@ -23,7 +23,8 @@ def test_header_declares_the_entry_points():
     syms = _declared_symbols()
     for s in ("sage_version", "sage_last_error", "sage_kv_prologue_workspace_bytes",
               "sage_kv_prologue", "sage_attn_fwd", "sage_attn_fwd_ex", "sage_attn_fwd_sk",
-              "sage_kseq_mean", "sage_kv_prologue_noalloc", "sage_quant_q", "sage_mfma_layout_probe"):
+              "sage_kseq_mean", "sage_kv_prologue_noalloc",
+              "sage_mfma_peak_probe", "sage_quant_q", "sage_mfma_layout_probe"):
         assert s in syms
 
 
@@ -102,6 +103,13 @@ def test_library_host_calls_without_a_gpu():
                                         64 * 128, 64 * 128, 128, 1, 4096, 64, 64, 128, p16, p16,
                                         p16, p16, None, None, p16, None, None)
     assert rc == 1 and b"scratch" in L.lib.sage_last_error()
+    # the MFMA probe's bounds
+    assert L.lib.sage_mfma_peak_probe(1, 0, 10, None, None) == 1
+    assert b"blocks" in L.lib.sage_last_error()
+    assert L.lib.sage_mfma_peak_probe(0, 8, 0, None, None) == 1
+    assert b"iters" in L.lib.sage_last_error()
+    assert L.lib.sage_mfma_peak_probe(0, 8, 8, ctypes.c_void_p(12), None) == 1
+    assert b"aligned" in L.lib.sage_last_error()
     # B*H beyond 65535 is a valid shape (the grids are 1-D); only the int32 block index bounds it
     rc = L.lib.sage_attn_fwd(0, 1, 0, p16, 8, 8, 8, None, None, None, None, p16, 8, 8, 8,
                              1, 70000, 100, 128, ctypes.c_float(0.1), None)
