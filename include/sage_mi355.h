@@ -47,6 +47,11 @@ int sage_version(void);
 /* Text of the last error on the calling thread ("" if none). Valid until the next call. */
 const char* sage_last_error(void);
 
+/* The build id: a hash of the sources and compiler flags this library was built from (computed by
+ * build_lib.py), so that a caller can tell a stale library from one built from its tree. No
+ * counterpart in the reference. */
+const char* sage_build_id(void);
+
 /*
  * Bytes of device workspace `sage_kv_prologue` (and `sage_kseq_mean`) needs for B*H planes of N
  * rows, for any N_pad. No reference counterpart: the reference allocates its mean with torch per

@@ -9,6 +9,7 @@ disabled (`-Xclang -target-feature -Xclang -packed-fp32-ops`).
 """
 import concurrent.futures
 import glob
+import hashlib
 import os
 import subprocess
 import sys
@@ -32,11 +33,31 @@ COMMON_FLAGS = [
 FILE_FLAGS = {
     "attn_fwd.hip": ["-fno-honor-nans"],
     "attn_fwd_pp.hip": ["-fno-honor-nans"],
+    "attn_fwd_pl.hip": ["-fno-honor-nans"],
 }
 
 
 def lib_path():
     return os.path.join(LIB_DIR, LIB_NAME)
+
+
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
+
+
+def source_hash():
+    """The build id: a SHA-256 prefix over every source the library is compiled from (csrc/*.hip,
+    csrc/*.h, include/*.h, by name and content) and the compiler flags. The library returns the
+    value it was built with from `sage_build_id()`, so a test can tell a stale library from one
+    built from the tree it runs in."""
+    h = hashlib.sha256()
+    files = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.h"))
+                   + glob.glob(os.path.join(INCLUDE, "*.h")))
+    for f in files:
+        h.update(os.path.relpath(f, os.path.dirname(HERE)).encode())
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+    h.update(repr((COMMON_FLAGS, sorted(FILE_FLAGS.items()))).encode())
+    return h.hexdigest()[:16]
 
 
 def _run(cmd, verbose):
@@ -62,8 +83,9 @@ def build(verbose=False, jobs=None):
     if not sources:
         raise RuntimeError("no HIP sources under %s" % CSRC)
     objs = [os.path.join(obj_dir, os.path.splitext(os.path.basename(s))[0] + ".o") for s in sources]
-    cmds = [[HIPCC] + COMMON_FLAGS + FILE_FLAGS.get(os.path.basename(s), []) + ["-c", s, "-o", o]
-            for s, o in zip(sources, objs)]
+    bid = ['-DSAGE_BUILD_ID="%s"' % source_hash()]
+    cmds = [[HIPCC] + COMMON_FLAGS + FILE_FLAGS.get(os.path.basename(s), []) + bid
+            + ["-c", s, "-o", o] for s, o in zip(sources, objs)]
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs or min(8, len(cmds))) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
     out = lib_path()

@@ -112,6 +112,11 @@ extern "C" {
 
 int sage_version(void) { return 100; }
 
+#ifndef SAGE_BUILD_ID
+#define SAGE_BUILD_ID "unknown"
+#endif
+const char* sage_build_id(void) { return SAGE_BUILD_ID; }
+
 const char* sage_last_error(void) { return g_err.c_str(); }
 
 size_t sage_kv_prologue_workspace_bytes(int64_t BH, int64_t N) {

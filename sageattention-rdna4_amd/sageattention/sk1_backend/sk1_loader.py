@@ -115,6 +115,8 @@ class SageLib:
         L.sage_version.argtypes = []
         L.sage_last_error.restype = ctypes.c_char_p
         L.sage_last_error.argtypes = []
+        L.sage_build_id.restype = ctypes.c_char_p
+        L.sage_build_id.argtypes = []
         L.sage_kv_prologue_workspace_bytes.restype = ctypes.c_size_t
         L.sage_kv_prologue_workspace_bytes.argtypes = [i64, i64]
         L.sage_kv_prologue.restype = i32
@@ -144,6 +146,7 @@ class SageLib:
         L.sage_mfma_peak_probe.restype = i32
         L.sage_mfma_peak_probe.argtypes = [i32, i64, i64, vp, vp]
         self.version = int(L.sage_version())
+        self.build_id = L.sage_build_id().decode()
         images = hip_runtime_images()
         self.hip_runtime = images
         self.same_as_torch = None if images is None else len(images) == 1

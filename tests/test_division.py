@@ -15,6 +15,10 @@ fp64; the final sum is rounded once with an exact two-sum and a midpoint check) 
 numpy's IEEE fp32 division on random, near-tie and boundary inputs. The GPU parity tests then hold
 the kernels' quantized tensors bit-exact against the oracle.
 """
+import os
+import shutil
+import subprocess
+
 import numpy as np
 import pytest
 
@@ -116,3 +120,51 @@ def test_emulation_detects_a_one_ulp_slip():
     ss = rng.uniform(0.01, 2, 100_000).astype(f32)
     q = (xs * (f32(1) / ss).astype(f32)).astype(f32)
     assert (q != (xs / ss).astype(f32)).any()
+
+
+@pytest.fixture(scope="module")
+def div_exhaustive(tmp_path_factory):
+    """tests/native/div_exhaustive.c built with gcc (OpenMP over the host's cores)."""
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    src = os.path.join(os.path.dirname(os.path.abspath(__file__)), "native", "div_exhaustive.c")
+    exe = str(tmp_path_factory.mktemp("divx") / "div_exhaustive")
+    subprocess.run([gcc, "-O2", "-fopenmp", "-o", exe, src, "-lm"], check=True)
+
+    def run(*args):
+        out = subprocess.run([exe] + [str(a) for a in args], check=True, capture_output=True,
+                             text=True, timeout=600).stdout
+        words = out.split("\n")[0].split()
+        return dict(zip(words[0::2], words[1::2])), out
+    return run
+
+
+def test_constant_divisor_127_exhaustive(div_exhaustive):
+    # every non-negative finite fp32 x (2^31 - 2^23 inputs): RN(x/127) bit for bit, subnormal
+    # quotients included -- the int8 scale max(RN(kmax/127), 1e-12)
+    r, out = div_exhaustive(127, 1e-12)
+    assert int(r["checked"]) == 0x7f800000
+    assert int(r["mismatches"]) == 0, out
+
+
+def test_constant_divisor_448_exhaustive(div_exhaustive):
+    # every non-negative finite fp32 x: RN(x/448) bit for bit wherever the quotient is a normal
+    # number; where it is subnormal (x < 448 * 2^-126) the correction step is not exact, but
+    # those quotients lie far below the scales' 1e-12 floor, so max(RN(x/448), 1e-12) -- the
+    # e4m3 scales sv and sk -- is exact for every x
+    r, out = div_exhaustive(448, 1e-12)
+    assert int(r["checked"]) == 0x7f800000
+    assert int(r["normal_quotient_mismatches"]) == 0, out
+    assert int(r["floored_mismatches"]) == 0, out
+    assert float.fromhex(r["max_bad_x"]) < 448 * 2.0 ** -126
+
+
+@pytest.mark.parametrize("variant", [1, 2], ids=["no_correction", "unfused_residual"])
+def test_exhaustive_check_catches_a_planted_mistake(div_exhaustive, variant):
+    # the plausible shortcuts -- q = RN(x * RN(1/s)) alone, or a residual formed with two
+    # roundings -- must show normal-range mismatches for both divisors (a reciprocal a few ulps
+    # off RN(1/s) does not: the exact-residual correction absorbs it)
+    for top in (127, 448):
+        r, out = div_exhaustive(top, 1e-12, variant)
+        assert int(r["normal_quotient_mismatches"]) > 0, out

@@ -155,3 +155,9 @@ def test_more_planes_than_a_grid_dimension():
         em = oracle.emulate_sageattn(qs, ks, vs, tensor_layout="HND", is_causal=causal)["o"]
         assert cosine(alone, em) >= 0.999 and rel_l1(alone, em) <= 1e-2
         assert torch.isfinite(out).all()
+
+
+def test_loaded_library_is_built_from_this_tree():
+    # on the GPU box the library is loaded as built here: its build id must be this tree's
+    import build_lib
+    assert _lib().build_id == build_lib.source_hash()

@@ -24,7 +24,8 @@ def test_header_declares_the_entry_points():
     for s in ("sage_version", "sage_last_error", "sage_kv_prologue_workspace_bytes",
               "sage_kv_prologue", "sage_attn_fwd", "sage_attn_fwd_ex", "sage_attn_fwd_sk",
               "sage_kseq_mean", "sage_kv_prologue_noalloc",
-              "sage_mfma_peak_probe", "sage_quant_q", "sage_mfma_layout_probe"):
+              "sage_mfma_peak_probe",
+              "sage_build_id", "sage_quant_q", "sage_mfma_layout_probe"):
         assert s in syms
 
 
@@ -239,3 +240,12 @@ def test_product_path_has_no_oracle_or_cpu_fallback():
                 src = open(os.path.join(dirpath, f)).read()
                 assert "oracle" not in src, f
                 assert "scaled_dot_product_attention" not in src, f
+
+
+def test_library_build_id_is_this_trees():
+    # the library reports the hash of the sources and flags it was compiled from; the loaded one
+    # must be this tree's (build_lib.source_hash), else it is stale
+    import build_lib
+    from sageattention.sk1_backend.sk1_loader import SageLib
+    bid = SageLib.get().build_id
+    assert len(bid) == 16 and bid == build_lib.source_hash()
