@@ -55,6 +55,9 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(attn_waves(D
   __shared__ StageBuf<D> sB0;
   __shared__ StageBuf<D> sB1;
   __shared__ StageBuf<D> sB2;
+  // q . mu of each query row, for the logsumexp's smooth_k correction: parked here rather than
+  // in a register that would live (and spill) across the whole loop
+  __shared__ float s_qmu[BM];
   constexpr int NDT = D / 32;   // 32-channel output tiles per wave
   constexpr int NKV = D / 64;   // 1 KB K and V^T requests per wave and block (each)
 
@@ -130,6 +133,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(attn_waves(D
                              sm_scale, qf, sq, cq,
                              (LSE && KMEAN) ? KMEAN + (int64_t)kvp * D : nullptr, &qmu);
   (void)sq;
+  if (LSE && hh == 0) s_qmu[32 * w + l32] = qmu;
   const float Sb = Sfold[kvp];
 
   f32x16 acc[NDT];
@@ -210,16 +214,22 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(attn_waves(D
   mfma_result_fence();
 
   // ---------- epilogue: O = acc * S / (l * 448) (+ V's mean with smooth_v, one fma) ----------
-  if (qrow < N) {
-    if (LSE && hh == 0) LSE[(int64_t)bh * N + qrow] = row_lse(mc, l_i, sm_scale, qmu);
+  // The row and lane half are formed again from the lane id (v_mbcnt), so that their values from
+  // the top of the kernel need not stay live across the loop.
+  const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int l32e = lane_e & 31, hhe = lane_e >> 5;
+  const int qrow_e = q0 + l32e;
+  if (qrow_e < N) {
+    if (LSE && hhe == 0)
+      LSE[(int64_t)bh * N + qrow_e] = row_lse(mc, l_i, sm_scale, s_qmu[32 * w + l32e]);
     const float inv = (l_i > 0.0f) ? __fdiv_rn(Sb, l_i * P_SCALE) : 0.0f;
-    T* op = O + b * o_sb + hd * o_sh + (int64_t)qrow * o_sr;
+    T* op = O + b * o_sb + hd * o_sh + (int64_t)qrow_e * o_sr;
     const float* vmp = VMEAN ? VMEAN + (int64_t)kvp * D : nullptr;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int d = 32 * dt + 8 * g + 4 * hh;
+        const int d = 32 * dt + 8 * g + 4 * hhe;
         T ov[4];
         if (vmp) {
           const float4 vm = *(const float4*)(vmp + d);

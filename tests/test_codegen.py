@@ -305,3 +305,37 @@ def test_mfma_results_are_read_after_the_mfma_completes(source):
     asm = _assembly(os.path.join(PKG, "csrc", source))
     bad = early_mfma_reads(asm)
     assert not bad, bad[:6]
+
+
+def _kernel_resources(asm):
+    """(kernel name, VGPRs, spilled VGPRs, scratch bytes per lane) for every kernel in hipcc's
+    metadata."""
+    out = []
+    for m in re.finditer(r"^\s+- \.agpr_count:.*?(?=^\s+- \.agpr_count:|^\.end_amdgpu_metadata)",
+                         asm, re.S | re.M):
+        block = m.group(0)
+        name = re.search(r"^\s+\.name:\s+(\S+)", block, re.M).group(1)
+        vg = int(re.search(r"^\s+\.vgpr_count:\s+(\d+)", block, re.M).group(1))
+        vs = int(re.search(r"^\s+\.vgpr_spill_count:\s+(\d+)", block, re.M).group(1))
+        ps = int(re.search(r"^\s+\.private_segment_fixed_size:\s+(\d+)", block, re.M).group(1))
+        out.append((name, vg, vs, ps))
+    return out
+
+
+@pytest.mark.parametrize("source", ["attn_fwd.hip", "attn_fwd_pp.hip", "attn_fwd_pl.hip",
+                                    "prologue.hip"])
+def test_no_kernel_spills_registers(source):
+    # the register budget is a gate: no instantiation of any kernel spills VGPRs or uses scratch
+    # memory at all (SGPRs parked in VGPR lanes, v_writelane, cost no memory traffic and are
+    # allowed)
+    res = _kernel_resources(_assembly(os.path.join(PKG, "csrc", source)))
+    assert res, "no kernel metadata found"
+    spilled = [r for r in res if r[2] or r[3]]
+    assert not spilled, spilled
+    assert max(r[1] for r in res) <= 256
+
+
+def test_resource_parser_sees_a_spill():
+    meta = ("  - .agpr_count:     0\n    .name:           _Zk\n    .private_segment_fixed_size: 12\n"
+            "    .vgpr_count:     168\n    .vgpr_spill_count: 3\n.end_amdgpu_metadata\n")
+    assert _kernel_resources(meta) == [("_Zk", 168, 3, 12)]
