@@ -13,4 +13,5 @@ from .sage_scheme import (  # noqa: F401
     BN, FLOOR, LOG2E, P_SCALE, I8_MAX,
     n_pad_for, kseq_mean, quant_k, quant_v, fold_v_scale, quant_q, attention_tiles,
     emulate_sageattn, exact_attention, exact_lse, kv_planes, row_lse, to_hnd,
+    vseq_mean_fp32_chunked,
 )

@@ -63,6 +63,41 @@ def kseq_mean(k):
     return (s / float(N)).to(torch.float32)
 
 
+def vseq_mean_fp32_chunked(x, chunk=1024, group=16):
+    """The sequence mean as the reference's own smooth_v path computes it: `kseq_mean_fp8`
+    (`sageattention/sk1_backend/quant_triton.py:303-373`), which its Triton prologue subtracts from V
+    under `SUB_VMEAN` (`quant_triton.py:714-719`).
+
+    Stage 1 (`_kseq_partial_sum`, `:303-331`): per chunk of `chunk` rows an fp32 accumulator, zeroed,
+    receives `group`-row sums in row order (`acc += tl.sum(x[16 rows], axis=0)`, rows past N
+    read as 0). Stage 2 (`_kseq_finalize_mean`, `:334-343`): the chunk partials summed in chunk order
+    in fp32, then one fp32 division by N. The order inside one 16-row `tl.sum` is Triton's
+    reduction tree, which the reference does not fix; it is taken here as a balanced pairwise tree
+    (rows 0+1, 2+3, ..., then pairs of pairs). So this restatement is the reference's definition up
+    to that order: parity at the bit level is unpinned, and it is used only at tolerance level.
+    `x`: (BH, N, D) fp16/bf16. Returns (BH, D) fp32.
+    """
+    BH, N, D = x.shape
+    xf = x.to(torch.float32)
+    n_ch = (N + chunk - 1) // chunk
+    parts = []
+    for c in range(n_ch):
+        acc = torch.zeros(BH, D, dtype=torch.float32)
+        for r in range(c * chunk, (c + 1) * chunk, group):
+            g = torch.zeros(BH, group, D, dtype=torch.float32)
+            hi = min(r + group, N)
+            if hi > r:
+                g[:, : hi - r] = xf[:, r:hi]
+            while g.shape[1] > 1:
+                g = g[:, 0::2] + g[:, 1::2]
+            acc = acc + g[:, 0]
+        parts.append(acc)
+    tot = torch.zeros(BH, D, dtype=torch.float32)
+    for p_ in parts:
+        tot = tot + p_
+    return tot / torch.tensor(float(N), dtype=torch.float32)
+
+
 def _pad_rows(x, n_pad):
     BH, N, D = x.shape
     out = torch.zeros(BH, n_pad, D, dtype=torch.float32)
@@ -267,7 +302,7 @@ def kv_planes(B, H, H_kv, N, N_kv, is_causal):
 
 
 def emulate_sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=None, smooth_k=True,
-                     qk_int8=None, smooth_v=False):
+                     qk_int8=None, smooth_v=False, vmean_def="fp64"):
     """The whole SK1 call on the CPU, returning every intermediate.
 
     Routing follows `sageattention/sk1_backend/__init__.py:1161-1272`: fp16 inputs use int8 Q.K
@@ -278,7 +313,8 @@ def emulate_sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=Non
     query plane b*H + h reads K/V plane `kv_planes(...)[b*H + h]`. `smooth_v` subtracts V's
     sequence mean (the same fp64-accumulated mean as K's) before quantizing V and adds it back in
     the epilogue (`quant_triton.py:668-678` of the reference; its shipped HIP prologue does not
-    compute V's mean).
+    compute V's mean). `vmean_def="fp32_chunked"` takes V's mean as the reference's Triton path
+    does instead (`vseq_mean_fp32_chunked`).
 
     Returns a dict with `mean, vmean, k8, sk, v8t, sv, s, svp, q8, sq, c_q, o, lse` where `o` has the
     caller's layout and dtype, `lse` is (B, H, N) fp32 (the `return_lse` output), `q8, sq, c_q`
@@ -298,7 +334,12 @@ def emulate_sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=Non
     kr, vr = (t.reshape(B * H_kv, N_kv, D) for t in (kk, vv))
     mean = kseq_mean(kr) if smooth_k else None
     k8, sk = quant_k(kr, n_pad, mean=mean, int8=qk_int8)
-    vmean = kseq_mean(vr) if smooth_v else None
+    if not smooth_v:
+        vmean = None
+    elif vmean_def == "fp32_chunked":
+        vmean = vseq_mean_fp32_chunked(vr)
+    else:
+        vmean = kseq_mean(vr)
     v8t, sv = quant_v(vr, n_pad, mean=vmean)
     s, svp = fold_v_scale(sv)
     q8, sq, c_q = quant_q(qr, sm, int8=qk_int8)

@@ -422,6 +422,28 @@ def test_smooth_v_matches_emulation(N, dtype, causal, layout):
         assert e_sv < e_plain
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N", [300, 4099])
+def test_smooth_v_against_the_reference_fp32_mean(N, dtype, causal):
+    # The reference's own smooth_v path takes V's mean in fp32 chunks (quant_triton.py:303-373,
+    # oracle.vseq_mean_fp32_chunked); this build takes it in fp64. Held to the same bars against
+    # an emulation that uses the reference's fp32 mean; and the prologue's VMEAN (the oracle's
+    # fp64 mean bit for bit, test_gpu_quant_parity) lies within the fp32 summation error of it.
+    q, k, v = make_qkv(1, 3, N, seed=N + 13, dtype=dtype, k_offset_std=2.0, v_offset_std=4.0)
+    print("N", N, dtype, causal, flush=True)
+    r = oracle.emulate_sageattn(q, k, v, is_causal=causal, smooth_v=True, vmean_def="fp32_chunked")
+    out = _sageattn()(q.cuda(), k.cuda(), v.cuda(), is_causal=causal, smooth_v=True).cpu()
+    cs, rl = cosine(out, r["o"]), rel_l1(out, r["o"])
+    print("cos %.6f rel_l1 %.2e" % (cs, rl))
+    assert cs >= COS_MIN and rl <= REL_L1_MAX, (cs, rl)
+    vr = v.reshape(3, N, 128)
+    ref32 = oracle.vseq_mean_fp32_chunked(vr).double()
+    ours = oracle.kseq_mean(vr).double()      # the prologue's VMEAN bits (bit-exact elsewhere)
+    bound = N * 2.0 ** -24 * vr.double().abs().mean(dim=1)
+    assert ((ours - ref32).abs() <= bound).all()
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_smooth_v_identical_rows_give_the_row_exactly(dtype):
     # every token's V equal to one vector c: the centred V is 0, so O = T(fma(0, inv, c)) = c

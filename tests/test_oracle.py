@@ -496,6 +496,60 @@ def test_gqa_and_kv_length_close_to_exact_attention():
 
 
 # ----------------------------------------------------------------------------- smooth_v
+def test_reference_fp32_chunked_mean_exact_on_integer_data():
+    # integer-valued rows: every fp32 partial sum is exact, so the reference's fp32 chunked mean
+    # (quant_triton.py:303-373) is RN32(sum / N), the correctly rounded mean -- the same bits as
+    # the fp64 mean this build uses, at lengths across chunk and 16-row group boundaries
+    g = torch.Generator().manual_seed(5)
+    for n in (1, 15, 16, 17, 1023, 1024, 1025, 3000):
+        x = torch.randint(-64, 65, (2, n, 8), generator=g).to(torch.float16)
+        a = oracle.vseq_mean_fp32_chunked(x)
+        b = oracle.kseq_mean(x)
+        want = torch.tensor([[float(np.float32(math.fsum(x[i, :, d].double().tolist()) / n))
+                              for d in range(8)] for i in range(2)], dtype=torch.float32)
+        assert torch.equal(a, want) and torch.equal(b, want), n
+
+
+def test_reference_fp32_chunked_mean_order_by_brute_force():
+    # a chunk is a sequence of 16-row group sums (each a pairwise tree), added in row order; the
+    # chunk partials are then added in chunk order and divided once, all in fp32 -- restated
+    # scalar by scalar with numpy fp32 on a small case (chunk 32, so three partial chunks)
+    g = torch.Generator().manual_seed(6)
+    x = (torch.randn(1, 70, 3, generator=g) * 1e3).to(torch.float16)
+    got = oracle.vseq_mean_fp32_chunked(x, chunk=32)
+    xf = x.float().numpy()
+    for d in range(3):
+        parts = []
+        for c in range(3):
+            acc = np.float32(0)
+            for r in range(32 * c, 32 * c + 32, 16):
+                vals = [xf[0, i, d] if i < 70 else np.float32(0) for i in range(r, r + 16)]
+                while len(vals) > 1:
+                    vals = [np.float32(vals[i] + vals[i + 1]) for i in range(0, len(vals), 2)]
+                acc = np.float32(acc + vals[0])
+            parts.append(acc)
+        tot = np.float32(0)
+        for p_ in parts:
+            tot = np.float32(tot + p_)
+        assert f32_bits(got[0, d].item()) == f32_bits(float(np.float32(tot / np.float32(70))))
+
+
+def test_fp64_mean_is_within_a_few_ulps_of_the_reference_fp32_mean():
+    # the build's V mean (fp64 sums, one rounding) against the reference's fp32 chunked mean on
+    # offset fp16 data at a long length: their difference is the fp32 summation error alone,
+    # bounded by N * 2^-24 * (sum |v|) / N per channel, and the fp64 mean is the closer of the two
+    # to the exact mean
+    g = torch.Generator().manual_seed(7)
+    n = 9000
+    x = (torch.randn(2, n, 16, generator=g) + 3.0).to(torch.float16)
+    a = oracle.vseq_mean_fp32_chunked(x).double()
+    b = oracle.kseq_mean(x).double()
+    exact = x.double().mean(dim=1)
+    bound = n * 2.0 ** -24 * x.double().abs().mean(dim=1)
+    assert ((a - b).abs() <= bound).all()
+    assert ((b - exact).abs() <= (a - exact).abs() + 1e-12).all()
+
+
 def test_smooth_v_mean_is_fsum_of_v_and_centering_precedes_the_scale():
     # V's mean is the same fp64 sequence mean as K's, and V is centred (fp32) before its absmax:
     # SV = max(RN(max_d |RN(v - mu)| / 448), 1e-12) on live rows, V8T the e4m3 of RN(RN(v - mu)/SV).
