@@ -18,7 +18,14 @@ Reference files (paths relative to the reference repository root):
 * `kernels/hip/sk1_t6i.hip` -- int8 Q.K main loop (fp16 inputs);
 * `kernels/hip/sk1_t4a1s.hip`, `kernels/hip/sk1_t4a1sb.hip` -- fp8 Q.K main loop (bf16 inputs);
 * `sageattention/sk1_backend/__init__.py` -- the per-(b,h) V-scale fold and the routing;
-* `sageattention/sk1_backend/hip_prologue.py` -- `n_pad_for`, the scale floor.
+* `sageattention/sk1_backend/hip_prologue.py` -- `n_pad_for`, the scale floor;
+* `sageattention/sk1_backend/quant_triton.py` -- the reference's fp32 sequence mean of its own
+  smooth_v path (`vseq_mean_fp32_chunked`).
+
+Parity status: every function here is pinned by `tests/test_oracle.py` and the golden fixtures,
+except `vseq_mean_fp32_chunked`, whose order inside one 16-row Triton reduction the reference does
+not fix: **parity unpinned** at the bit level for it (pinned on integer-valued rows, by a scalar
+brute force of the stated order, and against the fp64 mean within the fp32 summation bound).
 """
 import math
 
