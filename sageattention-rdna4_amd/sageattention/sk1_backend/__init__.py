@@ -16,11 +16,13 @@ Mirrors `sageattention/sk1_backend/__init__.py` of the reference (`ENVELOPE` `:3
 call is outside the envelope or (with `strict=False`) when the library fails.
 """
 import sys
+from contextlib import nullcontext
 
 import torch
 
 from .hip_prologue import HipPrologue, n_pad_for  # noqa: F401
-from .sk1_loader import STRIDED_REFUSALS, SageLib, strided_view_reason  # noqa: F401
+from .sk1_loader import (STRIDED_REFUSALS, SageLib, strided_view_reason,  # noqa: F401
+                         torch_stream)
 
 #: The architectures the library is built for.
 SUPPORTED_ARCHS = ("gfx950",)
@@ -188,36 +190,33 @@ def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=
     sm = float(sm_scale if sm_scale is not None else D ** -0.5)
     n_pad = n_pad_for(N_kv)
     dev = q.device
-    # the prologue's outputs are per K/V plane: B*H_kv planes of N_kv keys
-    k8 = torch.empty(BH_kv, n_pad, D, device=dev,
-                     dtype=torch.int8 if qk_int8 else torch.float8_e4m3fn)
-    sk = torch.empty(BH_kv, n_pad, device=dev, dtype=torch.float32)
-    v8t = torch.empty(BH_kv, D, n_pad, device=dev, dtype=torch.float8_e4m3fn)
-    sv = torch.empty(BH_kv, n_pad, device=dev, dtype=torch.float32)
-    s = torch.empty(BH_kv, device=dev, dtype=torch.float32)
-    kconst = torch.empty(BH_kv, n_pad // 64, 3, 64, device=dev, dtype=torch.float32)
-    ws = torch.empty(lib.workspace_bytes(BH_kv, N_kv), device=dev, dtype=torch.uint8)
+    # Every temporary of the call in one allocation, 256-byte aligned parts: the prologue's
+    # outputs per K/V plane (B*H_kv planes of N_kv keys) -- K8, SK, V8T, SV, S, KCONST -- its
+    # workspace, and K's mean (for the logsumexp) and V's mean (smooth_v) when used.
+    el8, nf = BH_kv * n_pad * D, BH_kv * n_pad * 4
+    ws_bytes = lib.workspace_bytes(BH_kv, N_kv)
+    parts = [("k8", el8), ("sk", nf), ("v8t", el8), ("sv", nf), ("s", BH_kv * 4),
+             ("kconst", 3 * nf), ("ws", ws_bytes)]
+    if return_lse and smooth_k:
+        parts.append(("kmean", BH_kv * D * 4))
+    if smooth_v:
+        parts.append(("vmean", BH_kv * D * 4))
+    off, total = {}, 0
+    for name, nbytes in parts:
+        off[name] = total
+        total += (nbytes + 255) // 256 * 256
+    tmp = torch.empty(total, device=dev, dtype=torch.uint8)
     lse = torch.empty(B, H, N, device=dev, dtype=torch.float32) if return_lse else None
-    kmean = (torch.empty(BH_kv, D, device=dev, dtype=torch.float32)
-             if (return_lse and smooth_k) else None)
-    vmean = torch.empty(BH_kv, D, device=dev, dtype=torch.float32) if smooth_v else None
     if tensor_layout == "NHD":
         out = torch.empty(B, N, H, D, device=dev, dtype=q.dtype)
         oo = out.transpose(1, 2)
     else:
         out = torch.empty(B, H, N, D, device=dev, dtype=q.dtype)
         oo = out
-    with torch.cuda.device(dev):
-        if events is not None:
-            events[0].record()
-        lib.kv_prologue(kk, vv, k8, sk, v8t, sv, s, kmean, ws, k_int8=qk_int8,
-                        smooth_k=bool(smooth_k), fold=True, n_pad=n_pad, kconst=kconst,
-                        smooth_v=bool(smooth_v), vmean=vmean)
-        if events is not None:
-            events[1].record()
-        lib.attn_fwd(qq, k8, kconst, v8t, s, oo, qk_int8=qk_int8, causal=bool(is_causal),
-                     sm_scale=sm, n_pad=n_pad, kernel=kernel, lse=lse, kmean=kmean, n_kv=N_kv,
-                     vmean=vmean)
-        if events is not None:
-            events[2].record()
+    ctx = torch.cuda.device(dev) if dev.index != torch.cuda.current_device() else nullcontext()
+    with ctx:
+        lib.prologue_and_main(qq, kk, vv, oo, tmp.data_ptr(), off, ws_bytes, n_pad,
+                              qk_int8=qk_int8, smooth_k=bool(smooth_k), smooth_v=bool(smooth_v),
+                              causal=bool(is_causal), sm_scale=sm, kernel=kernel, lse=lse,
+                              stream=torch_stream(dev), events=events)
     return (out, lse) if return_lse else out

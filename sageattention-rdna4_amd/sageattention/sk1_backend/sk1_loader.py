@@ -42,9 +42,13 @@ def strided_view_reason(t, name="t"):
     """
     if t.dim() != 4:
         return "rank"
+    st = t.stride()
+    if t.is_contiguous() and st[3] == 1 and st[0] > 0 and st[1] > 0 and st[2] > 0 \
+            and not ((st[0] | st[1] | st[2]) & 7) and not (t.data_ptr() & 15):
+        return None   # row-major with positive strides: an injective index map
     if int(t.stride(3)) != 1:
         return "stride_last"
-    st = [int(s) for s in t.stride()]
+    st = [int(s) for s in st]
     if any(s <= 0 for s in st):
         return "stride_nonpos"
     if any(st[i] % 8 for i in (0, 1, 2)):
@@ -179,6 +183,43 @@ class SageLib:
             int(workspace.numel() * workspace.element_size()),
             ctypes.c_void_p(torch_stream(k.device)))
         self._check(rc, "sage_kv_prologue")
+
+    def prologue_and_main(self, q, k, v, o, base, off, ws_bytes, n_pad, *, qk_int8, smooth_k,
+                          smooth_v, causal, sm_scale, kernel, lse, stream, events=None):
+        """The served call's two library calls (`sage_kv_prologue`, then `sage_attn_fwd_ex`) on
+        one device buffer that holds every temporary: K8, SK, V8T, SV, S, KCONST and the workspace
+        (and KMEAN, VMEAN when present) at the byte offsets `off[name]` from address `base`.
+        `q`, `o` are logical (B, H, N, D) views, `k`, `v` (B, H_kv, N_kv, D). One stream handle for
+        both calls; `events` (three, optional) are recorded before, between and after them."""
+        B, H, N, D = q.shape
+        H_kv, N_kv = k.shape[1], k.shape[2]
+        vp = ctypes.c_void_p
+
+        def at(name):
+            o_ = off.get(name)
+            return None if o_ is None else vp(base + o_)
+
+        dt = _dtype_code(q.dtype)
+        st = vp(stream)
+        ks, vs, qs, os_ = k.stride(), v.stride(), q.stride(), o.stride()
+        if events is not None:
+            events[0].record()
+        rc = self.lib.sage_kv_prologue(
+            dt, int(qk_int8), int(smooth_k), int(smooth_v), 1, vp(k.data_ptr()), ks[0], ks[1],
+            ks[2], vp(v.data_ptr()), vs[0], vs[1], vs[2], B, H_kv, N_kv, n_pad, D, at("k8"),
+            at("sk"), at("v8t"), at("sv"), at("kmean"), at("vmean"), at("s"), at("kconst"),
+            at("ws"), ws_bytes, st)
+        self._check(rc, "sage_kv_prologue")
+        if events is not None:
+            events[1].record()
+        rc = self.lib.sage_attn_fwd_ex(
+            dt, int(qk_int8), int(causal), vp(q.data_ptr()), qs[0], qs[1], qs[2], at("k8"),
+            at("kconst"), at("v8t"), at("s"), vp(o.data_ptr()), os_[0], os_[1], os_[2], B, H, N,
+            H_kv, N_kv, n_pad, D, ctypes.c_float(sm_scale), int(kernel), _ptr(lse), at("kmean"),
+            at("vmean"), st)
+        self._check(rc, "sage_attn_fwd")
+        if events is not None:
+            events[2].record()
 
     def kv_prologue_noalloc(self, k, v, k8, sk, v8t, sv, s, mean, *, k_int8, smooth_k, fold,
                             n_pad, kconst=None, smooth_v=False, vmean=None):
