@@ -175,7 +175,17 @@ def cpu_baseline(wl, q, k, v, budget_s=20.0):
     fixed = max(te1 + ts1 - 64 * per_row, 0.0)
     rows = int(min(N, max(64.0, (budget_s - fixed) / per_row)) // 64 * 64) or 64
     ops, te, ts = run(rows)
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     return dict(value=ops / te / 1e9, unit="GOPS", cores=torch.get_num_threads(), kind="port",
+                cpu_model=model, torch_version=torch.__version__,
                 sample="plane 0 of %d, last %d query rows of N=%d%s, with that plane's prologue; "
                        "ops %.3e, emulation %.2f s" % (B * H, rows, N, " (causal)" if causal else "",
                                                        ops, te),
@@ -233,8 +243,8 @@ def settle(call, sync, *, min_calls=40, min_s=4.0, max_s=10.0, chunk_s=0.5, max_
 def aa_twin(call, make_event, sync, *, rounds=10, batch=5):
     """The A/A twin (`docs/METHOD.md:14-22`): the same call measured as two candidates, A and B,
     over `rounds` interleaved rounds with the order swapped every round; each measurement is one
-    event pair around a batch of `batch` calls. Returns both medians (ms per call) and their
-    ratio B/A, whose distance from 1 is the run's noise floor."""
+    event pair around a batch of `batch` calls. Returns both medians (ms per call), their ratio
+    B/A (whose distance from 1 is the run's noise floor) and each candidate's min-max."""
     import statistics
     res = {"A": [], "B": []}
     for r in range(rounds):
@@ -248,7 +258,9 @@ def aa_twin(call, make_event, sync, *, rounds=10, batch=5):
             res[name].append(e0.elapsed_time(e1) / batch)
     ma, mb = statistics.median(res["A"]), statistics.median(res["B"])
     return {"rounds": rounds, "batch": batch, "ms_a": round(ma, 4), "ms_b": round(mb, 4),
-            "ratio": round(mb / ma, 4)}
+            "ratio": round(mb / ma, 4),
+            "range_a": [round(min(res["A"]), 4), round(max(res["A"]), 4)],
+            "range_b": [round(min(res["B"]), 4), round(max(res["B"]), 4)]}
 
 
 def mfma_peak(lib, qk_int8, make_event, sync, *, target_ms=25.0, reps=5):

@@ -151,3 +151,6 @@ def test_aa_twin_interleaves_and_reports_medians(bench):
     # (a sequential A-then-B would report B ~25 % faster)
     assert abs(aa["ratio"] - 1.0) < 0.05
     assert 5.0 < aa["ms_a"] < 10.0 and 5.0 < aa["ms_b"] < 10.0
+    for k in ("range_a", "range_b"):
+        lo, hi = aa[k]
+        assert lo <= hi and lo <= aa["ms_" + k[-1]] <= hi
