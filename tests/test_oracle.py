@@ -625,3 +625,22 @@ def test_smooth_v_wins_on_offset_v_and_the_add_back_is_needed(monkeypatch):
     monkeypatch.setattr(mod, "attention_tiles", ns["attention_tiles"])
     err_planted = (mod.emulate_sageattn(q, k, v, smooth_v=True)["o"].double() - ex).abs().max().item()
     assert err_planted > 1.0
+
+
+# ----------------------------------------------------------------------------- row subsets
+@pytest.mark.parametrize("causal", [True, False])
+def test_row_subset_equals_the_full_emulation(causal):
+    """`attention_tiles(..., row0=r)` over a slice of query rows gives those rows of the whole
+    emulation bit for bit (the long-sequence GPU test checks only a few rows this way)."""
+    N = 300
+    q, k, v = make_qkv(1, 1, N, seed=11, k_offset_std=2.0)
+    full = oracle.emulate_sageattn(q, k, v, is_causal=causal)["o"][0, 0]
+    kr, vr = k[0], v[0]
+    n_pad = oracle.n_pad_for(N)
+    k8, sk = oracle.quant_k(kr, n_pad, mean=oracle.kseq_mean(kr), int8=True)
+    v8t, sv = oracle.quant_v(vr, n_pad)
+    s, svp = oracle.fold_v_scale(sv)
+    for r0, r1 in ((0, 7), (100, 165), (N - 64, N)):
+        q8, _, cq = oracle.quant_q(q[0][:, r0:r1], 128 ** -0.5, int8=True)
+        part = oracle.attention_tiles(q8, cq, k8, sk, v8t, svp, s, N, causal, q.dtype, row0=r0)
+        assert torch.equal(part[0], full[r0:r1]), (r0, r1)
