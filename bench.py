@@ -360,11 +360,9 @@ def main():
     else:
         call = split_call
         timed_call = "sk1_forward(kernel=%d)" % args.kernel
-    # the library's choice by size (sage_attn_fwd_ex): 256 queries per block from N = 32768 on,
-    # head_dim 128 only
-    q256 = args.kernel == 2 or (args.kernel == 0 and N >= 32768 and D == 128)
-    kname = ("attn_fwd_pl_kernel" if args.kernel == 3 else
-             "attn_fwd_pp_kernel" if q256 else "attn_fwd_kernel")
+    # the kernel the timed call runs: the library's own automatic choice for kernel 0
+    kcode = args.kernel or lib.kernel_choice(B, H, N, D, causal)
+    kname = {1: "attn_fwd_kernel", 2: "attn_fwd_pp_kernel", 3: "attn_fwd_pl_kernel"}[kcode]
     sync = torch.cuda.synchronize
     event = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     for _ in range(args.warmup):

@@ -36,7 +36,7 @@ extern "C" {
 #define SAGE_BF16 1
 
 /* main-loop kernel choice of sage_attn_fwd_ex (all give the same bits) */
-#define SAGE_KERNEL_AUTO 0  /* by size: the 256-query ping-pong from N = 32768 on, else 128 */
+#define SAGE_KERNEL_AUTO 0  /* by grid fill on this device: sage_attn_kernel_choice */
 #define SAGE_KERNEL_Q128 1  /* 128 queries per block of 4 waves */
 #define SAGE_KERNEL_Q256 2  /* 256 queries per block of 8 waves, two groups in ping-pong */
 #define SAGE_KERNEL_PIPE 3  /* 128 queries per block of 4 waves, MFMAs pipelined inside each wave */
@@ -161,7 +161,7 @@ int sage_attn_fwd(int dtype, int qk_int8, int causal,
  * choice has no counterpart in the reference (one kernel per dtype there).
  *
  *   q, o      logical (B, H, N, D) views, as in sage_attn_fwd
- *   D         head_dim, 64 or 128; 64 runs the 128-query kernel (SAGE_KERNEL_Q256 is refused)
+ *   D         head_dim, 64 or 128 (at 64, SAGE_KERNEL_Q256 is refused)
  *   k8, kconst, v8t, s   the prologue's outputs for B*H_kv planes of N_kv keys (N_kv_pad =
  *             ceil(N_kv/64)*64). Query head h reads K/V head h / (H / H_kv) (grouped-query and
  *             multi-query attention; H must be a multiple of H_kv), and N may differ from N_kv
@@ -189,6 +189,20 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal,
                      int64_t B, int64_t H, int64_t N, int64_t H_kv, int64_t N_kv,
                      int64_t N_kv_pad, int64_t D, float sm_scale, int kernel,
                      float* lse, const float* kmean, const float* vmean, void* stream);
+
+/*
+ * The main-loop kernel SAGE_KERNEL_AUTO runs for a call of this shape: SAGE_KERNEL_Q256 or
+ * SAGE_KERNEL_PIPE (all kernels give the same bits; only speed differs). No counterpart in the
+ * reference (one kernel per dtype there); for benchmarks and profilers that name the kernel.
+ *   cus  compute units to plan for; <= 0: those of the current device (a device query)
+ * head_dim 64 runs the pipelined kernel. At 128 the 256-query ping-pong runs when, on `cus` CUs,
+ * its grid is estimated to finish at least 3 % sooner: a causal grid with at least 4 of its
+ * blocks per CU; a non-causal one by whole rounds of blocks (up to three 128-query blocks or one
+ * 256-query block resident per CU) at per-CU throughputs measured on MI355X.
+ * Returns the kernel code, or -SAGE_ERR_INVALID for a bad shape or head_dim, or -SAGE_ERR_HIP
+ * when the device query fails.
+ */
+int sage_attn_kernel_choice(int64_t B, int64_t H, int64_t N, int64_t D, int causal, int64_t cus);
 
 /*
  * The main loop on the reference kernel's own inputs: per-key scales SK (B*H_kv, N_kv_pad) and

@@ -4,6 +4,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
 #include <mutex>
 #include <string>
 
@@ -106,9 +107,68 @@ int scratch_for_current_device(void** out) {
   return SAGE_OK;
 }
 
+// Compute units of the current device, looked up once per device.
+std::atomic<int> g_cus[kMaxDevices];
+
+int cus_of_current_device(int64_t* out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(SAGE_ERR_INVALID, "device %d beyond the %d the library tracks", dev, kMaxDevices);
+  int n = g_cus[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return hip_status(e, "hipDeviceGetAttribute(multiprocessor count)");
+    if (n <= 0) return fail(SAGE_ERR_HIP, "device %d reports %d compute units", dev, n);
+    g_cus[dev].store(n, std::memory_order_relaxed);
+  }
+  *out = n;
+  return SAGE_OK;
+}
+
+// Estimated makespans of a non-causal grid, in units of one 128-query block's work run alone on a
+// CU. Every block of a non-causal grid does the same work, and the dispatcher keeps each CU's
+// slots full, so the grid runs in rounds. Per-CU throughputs, measured on MI355X (B*H = 8 and 48,
+// N = 288 .. 32768, both kernels timed on one box): the 128-query kernels with 1, 2 or 3 blocks
+// resident on a CU (one to three waves per SIMD) 1.00, 1.52 and 1.69; the 256-query ping-pong
+// (one block per CU) 1.75 blocks of 128 queries.
+double est_q128(int64_t blocks, int64_t cus) {
+  static const double rate[4] = {0.0, 1.0, 1.52, 1.69};
+  const int64_t full = blocks / (3 * cus), rem = blocks - full * 3 * cus;
+  double t = (double)full * 3.0 / rate[3];
+  if (rem) {
+    const int64_t k = (rem + cus - 1) / cus;
+    t += (double)k / rate[k];
+  }
+  return t;
+}
+double est_q256(int64_t blocks, int64_t cus) { return (double)((blocks + cus - 1) / cus) * 2.0 / 1.75; }
+
+int kernel_for(int64_t B, int64_t H, int64_t N, int64_t D, int causal, int64_t cus) {
+  if (D != 128) return SAGE_KERNEL_PIPE;
+  const int64_t nb256 = B * H * ((N + 255) / 256);
+  if (causal) return nb256 >= 4 * cus ? SAGE_KERNEL_Q256 : SAGE_KERNEL_PIPE;
+  const int64_t nb128 = B * H * ((N + 127) / 128);
+  return est_q256(nb256, cus) < 0.97 * est_q128(nb128, cus) ? SAGE_KERNEL_Q256 : SAGE_KERNEL_PIPE;
+}
+
 }  // namespace
 
 extern "C" {
+
+int sage_attn_kernel_choice(int64_t B, int64_t H, int64_t N, int64_t D, int causal, int64_t cus) {
+  if (B < 1 || H < 1 || N < 1)
+    return -fail(SAGE_ERR_INVALID, "shape: B, H and N must be positive (B=%lld H=%lld N=%lld)",
+                 (long long)B, (long long)H, (long long)N);
+  if (D != 64 && D != 128) return -fail(SAGE_ERR_INVALID, "head_dim: %lld is not 64 or 128", (long long)D);
+  if (cus <= 0) {
+    const int rc = cus_of_current_device(&cus);
+    if (rc) return -rc;
+  }
+  return kernel_for(B, H, N, D, causal, cus);
+}
+
 
 int sage_version(void) { return 100; }
 
@@ -268,16 +328,20 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
   a.lse = lse;
   a.kmean = lse ? kmean : nullptr;
   a.vmean = vmean;
-  // The 256-query ping-pong pays off on long sequences; at shorter ones its larger tiles leave too
-  // few blocks per CU and more causal diagonal work, and the 128-query kernel (three waves per
-  // SIMD) is faster: measured 3 % faster at N = 16384, 3 % slower at N = 47520.
-  const bool q256 = kernel == SAGE_KERNEL_Q256 ||
-                    (kernel == SAGE_KERNEL_AUTO && D == 128 && N >= 32768 && N_kv >= 32768);
+  // SAGE_KERNEL_AUTO: the kernel the grid-fill rule picks for this device (kernel_for)
+  if (kernel == SAGE_KERNEL_AUTO) {
+    int64_t cus = 0;
+    if ((rc = cus_of_current_device(&cus))) return rc;
+    kernel = kernel_for(B, H, N, D, causal, cus);
+  }
+  hipError_t e;
   if (kernel == SAGE_KERNEL_PIPE)
-    return hip_status(sage::launch_attn_fwd_pl(a, (hipStream_t)stream), "sage_attn_fwd launch");
-  return hip_status(q256 ? sage::launch_attn_fwd_pp(a, (hipStream_t)stream)
-                         : sage::launch_attn_fwd(a, (hipStream_t)stream),
-                    "sage_attn_fwd launch");
+    e = sage::launch_attn_fwd_pl(a, (hipStream_t)stream);
+  else if (kernel == SAGE_KERNEL_Q256)
+    e = sage::launch_attn_fwd_pp(a, (hipStream_t)stream);
+  else
+    e = sage::launch_attn_fwd(a, (hipStream_t)stream);
+  return hip_status(e, "sage_attn_fwd launch");
 }
 
 int sage_attn_fwd_sk(int dtype, int qk_int8, int causal, const void* q, int64_t q_sb,

@@ -149,6 +149,8 @@ class SageLib:
         L.sage_mfma_layout_probe.argtypes = [vp] * 7
         L.sage_mfma_peak_probe.restype = i32
         L.sage_mfma_peak_probe.argtypes = [i32, i64, i64, vp, vp]
+        L.sage_attn_kernel_choice.restype = i32
+        L.sage_attn_kernel_choice.argtypes = [i64, i64, i64, i64, i32, i64]
         self.version = int(L.sage_version())
         self.build_id = L.sage_build_id().decode()
         images = hip_runtime_images()
@@ -165,6 +167,16 @@ class SageLib:
 
     def workspace_bytes(self, BH, N):
         return int(self.lib.sage_kv_prologue_workspace_bytes(int(BH), int(N)))
+
+    def kernel_choice(self, B, H, N, D, causal, cus=0):
+        """The main-loop kernel code (2: 256-query ping-pong, 3: pipelined) the library's
+        automatic choice runs for this shape on `cus` compute units (0: the current device's;
+        see `sage_attn_kernel_choice`)."""
+        rc = int(self.lib.sage_attn_kernel_choice(int(B), int(H), int(N), int(D), int(bool(causal)),
+                                                  int(cus)))
+        if rc < 0:
+            self._check(-rc, "sage_attn_kernel_choice")
+        return rc
 
     # ------------------------------------------------------------------ entry points
     def kv_prologue(self, k, v, k8, sk, v8t, sv, s, mean, workspace, *, k_int8, smooth_k, fold,

@@ -253,12 +253,21 @@ def test_q256_kernel_nhd_equals_hnd_bitwise():
     assert torch.equal(o_nhd.transpose(1, 2), o_hnd)
 
 
-def test_auto_kernel_choice_serves_long_sequences():
-    # N = 32768 takes the 256-query kernel by default; it must equal the 128-query kernel there.
-    q, k, v = make_qkv(1, 1, 32768, seed=21, dtype=torch.float16, k_offset_std=2.0)
-    o_auto = _forward(q, k, v, causal=True, kernel=0)
-    o128 = _forward(q, k, v, causal=True, kernel=1)
-    assert torch.equal(o_auto, o128)
+@pytest.mark.parametrize("H,N,causal", [(8, 8192, False), (1, 32768, True), (2, 700, False)])
+def test_auto_kernel_choice_runs_the_kernel_it_names(H, N, causal):
+    # The automatic choice runs the kernel sage_attn_kernel_choice names for this device, and
+    # gives the 128-query kernel's bits.
+    from sageattention.sk1_backend.sk1_loader import SageLib
+    lib = SageLib.get()
+    code = lib.kernel_choice(1, H, N, 128, causal)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert code == lib.kernel_choice(1, H, N, 128, causal, cus=cus)
+    if cus == 256:
+        assert code == {(8, 8192, False): 2, (1, 32768, True): 3, (2, 700, False): 3}[(H, N, causal)]
+    q, k, v = make_qkv(1, H, N, seed=21, dtype=torch.float16, k_offset_std=2.0)
+    o_auto = _forward(q, k, v, causal=causal, kernel=0)
+    assert torch.equal(o_auto, _forward(q, k, v, causal=causal, kernel=code))
+    assert torch.equal(o_auto, _forward(q, k, v, causal=causal, kernel=1))
 
 
 # ---------------------------------------------------------------------------------------------

@@ -24,7 +24,7 @@ def test_header_declares_the_entry_points():
     for s in ("sage_version", "sage_last_error", "sage_kv_prologue_workspace_bytes",
               "sage_kv_prologue", "sage_attn_fwd", "sage_attn_fwd_ex", "sage_attn_fwd_sk",
               "sage_kseq_mean", "sage_kv_prologue_noalloc",
-              "sage_mfma_peak_probe",
+              "sage_mfma_peak_probe", "sage_attn_kernel_choice",
               "sage_build_id", "sage_quant_q", "sage_mfma_layout_probe"):
         assert s in syms
 
@@ -40,6 +40,42 @@ def test_library_loads_and_exports_every_declared_symbol():
                          text=True).stdout
     exported = set(re.findall(r" T (sage_\w+)", out))
     assert exported == set(_declared_symbols())
+
+
+def test_kernel_choice_by_grid_fill():
+    # The automatic main-loop choice on 256 CUs (no device query when the CU count is given).
+    # Causal: the 256-query ping-pong from 4 of its blocks per CU (1024 blocks). Non-causal: whole
+    # rounds of blocks (three 128-query blocks or one 256-query block per CU) at the measured
+    # per-CU throughputs 1.00 / 1.52 / 1.69 and 1.75; the ping-pong when >= 3 % sooner.
+    from sageattention.sk1_backend import sk1_loader
+    if not os.path.isfile(sk1_loader.LIB_PATH):
+        pytest.skip("library not built")
+    L = sk1_loader.SageLib.get()
+    Q256, PIPE = 2, 3
+    cases = [
+        # (B, H, N, D, causal, expected)
+        (1, 48, 47520, 128, True, Q256),    # the headline: 8928 blocks of 256 queries
+        (1, 48, 47520, 64, True, PIPE),     # head_dim 64: always the pipelined kernel
+        (1, 48, 4096, 128, True, PIPE),     # 768 blocks < 1024
+        (1, 8, 32768, 128, True, Q256),     # exactly 1024 blocks
+        (1, 8, 32512, 128, True, PIPE),     # 1016 blocks
+        # non-causal, in units of one 128-query block alone on a CU:
+        (1, 48, 1024, 128, False, Q256),    # 384 blocks: two on half the CUs, 2/1.52 = 1.32;
+                                            # 192 blocks of 256 in one round: 2/1.75 = 1.14
+        (1, 48, 512, 128, False, PIPE),     # 192 blocks, one per CU: 1.00 against 1.14
+        (1, 48, 2048, 128, False, PIPE),    # one round of three, 3/1.69 = 1.78 against 2.29
+        (1, 48, 8771, 128, False, PIPE),    # 4 rounds of three + 1 block: 8.10 against 7 x 1.14
+                                            # = 8.00, not 3 % sooner
+        (1, 48, 47520, 128, False, Q256),   # 23 x 1.78 + 1 = 41.8 against 35 x 1.14 = 40.0
+        (1, 8, 8192, 128, False, Q256),     # 512 blocks: 1.32 against one round, 1.14
+        (1, 8, 12288, 128, False, PIPE),    # one round of three: 1.78 against 2.29
+    ]
+    for B, H, N, D, causal, want in cases:
+        assert L.kernel_choice(B, H, N, D, causal, cus=256) == want, (B, H, N, D, causal)
+    with pytest.raises(ValueError, match="shape"):
+        L.kernel_choice(0, 48, 1024, 128, False, cus=256)
+    with pytest.raises(ValueError, match="head_dim"):
+        L.kernel_choice(1, 48, 1024, 96, False, cus=256)
 
 
 def test_library_host_calls_without_a_gpu():
