@@ -97,9 +97,9 @@ int sage_kseq_mean(int dtype, const void* k, int64_t k_sb, int64_t k_sh, int64_t
  *             `sageattention/sk1_backend/__init__.py:208-229`)
  *   outputs   k8, sk, v8t, sv, s (required); mean (may be NULL; written when smooth_k);
  *             vmean (B*H, 128) fp32 (required with smooth_v, else unused);
- *             kconst (may be NULL): the main loop's per-key constants, (B*H, N_pad/64, 3, 64) fp32:
- *             for each 64-key block SK, the fma addend -RN(1.5*2^23*SK) (0 when !k_int8) and
- *             RN(SV'*448) -- a layout of SK and SV' (no reference counterpart: the reference's
+ *             kconst (may be NULL): the main loop's per-key constants, (B*H, N_pad/64, 2, 64) fp32:
+ *             for each 64-key block SK and RN(SV'*448) -- a layout of SK and SV' that the main
+ *             loop stages in one piece per block (no reference counterpart: the reference's
  *             kernel derives them from SK/SV itself, `kernels/hip/sk1_t6i.hip:189-207`, `:249-262`)
  *   workspace at least sage_kv_prologue_workspace_bytes(B*H, N) bytes, 256-byte aligned
  */

@@ -199,9 +199,9 @@ __device__ __forceinline__ void qk_block(const u8* __restrict__ kbuf, const QFra
 // loops, which convert the zero-seeded int32 dot product instead) and RN(SV' * 448).
 struct ScaleTile {
   float sk[BK];
-  float nsk[BK];
   float w[BK];
-  float pad[BK];   // landing area of the fourth wave's copy (keeps every wave's request count equal)
+  float pad[2 * BK];   // landing area of the 128-query kernel's waves 2 and 3, whose copies keep
+                       // every wave's request count equal
 };
 
 // Max of 32 values as 16 three-input maxima (v_max3_f32), a tree of depth 4.

@@ -79,7 +79,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(attn_waves(D
 
   const u8* Kb = K8 + (int64_t)kvp * Nk_pad * D;
   const u8* Vb = V8T + (int64_t)kvp * D * Nk_pad;
-  const float* KCb = KC + (int64_t)kvp * Nk_pad * 3;   // 192 floats per 64-key block
+  const float* KCb = KC + (int64_t)kvp * Nk_pad * 2;   // 128 floats per 64-key block
 
   const int n_blocks = Nk_pad / BK;
   const int j_end = CAUSAL ? min(n_blocks, (qt * BM + BM - 1) / BK + 1) : n_blocks;
@@ -96,8 +96,8 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(attn_waves(D
   //        holds logical chunk slot ^ kswz(row).
   //   V^T: request I carries rows d = 16I..16I+15; lane l -> row 16I + l/4, slot l%4 holding
   //        logical chunk (l%4) ^ vswz(d).
-  //   KC:  waves 0..2 carry floats 64w..64w+63 of the block's 192 (4 B/lane); wave 3 repeats
-  //        wave 0's into the tile's pad.
+  //   KC:  waves 0 and 1 carry floats 64w..64w+63 of the block's 128 (4 B/lane); waves 2 and 3
+  //        repeat them into the tile's pad.
   uint32_t k_off[NKV], v_off[NKV];
 #pragma unroll
   for (int i = 0; i < NKV; ++i) {
@@ -107,12 +107,12 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(attn_waves(D
     const int d = 16 * I + (lane >> 2), vpos = lane & 3;
     v_off[i] = (uint32_t)(d * Nk_pad + 16 * (vpos ^ vswz(d)));
   }
-  const uint32_t c_off = (uint32_t)(4 * (64 * (w == 3 ? 0 : w) + lane));
+  const uint32_t c_off = (uint32_t)(4 * (64 * (w & 1) + lane));
   const uint32_t c_dst = (uint32_t)(256 * w);
   auto dma = [&](int j, StageBuf<D>& buf) {
     const u8* kblk = Kb + (size_t)(BK * D) * (uint32_t)j;
     const u8* vblk = Vb + (size_t)BK * (uint32_t)j;
-    const u8* cblk = (const u8*)KCb + (size_t)(192 * 4) * (uint32_t)j;
+    const u8* cblk = (const u8*)KCb + (size_t)(128 * 4) * (uint32_t)j;
     const uint32_t kl = lds_addr(buf.k) + 1024 * NKV * w, vl = lds_addr(buf.v) + 1024 * NKV * w;
 #pragma unroll
     for (int i = 0; i < NKV; ++i) dma16(kblk, k_off[i], kl + 1024 * i);

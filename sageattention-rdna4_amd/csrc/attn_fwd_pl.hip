@@ -347,8 +347,8 @@ static void launch_pl_d(const AttnArgs& a, hipStream_t stream) {
   // per-key constant rows: the reference's SK / SV' arrays, or the prologue's KCONST layout
   const bool kc = a.kconst != nullptr;
   const float* skr = kc ? a.kconst : a.sk;
-  const float* wr = kc ? a.kconst + 2 * BK : a.svp;
-  const int64_t plane = kc ? 3 * a.N_kv_pad : a.N_kv_pad, blk = kc ? 3 * BK : BK;
+  const float* wr = kc ? a.kconst + BK : a.svp;
+  const int64_t plane = kc ? 2 * a.N_kv_pad : a.N_kv_pad, blk = kc ? 2 * BK : BK;
   hipLaunchKernelGGL((attn_fwd_pl_kernel<T, QK_INT8, CAUSAL, D>), dim3(total), dim3(AT), 0, stream,
                      (const T*)a.q, (const u8*)a.k8, skr, plane, blk, wr, plane, blk,
                      kc ? 1.0f : P_SCALE, (const u8*)a.v8t, a.s, (T*)a.o, a.q_sb, a.q_sh, a.q_sr,

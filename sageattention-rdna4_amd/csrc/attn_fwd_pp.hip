@@ -61,7 +61,7 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
 
   const u8* Kb = K8 + (int64_t)kvp * Nk_pad * HD;
   const u8* Vb = V8T + (int64_t)kvp * HD * Nk_pad;
-  const float* KCb = KC + (int64_t)kvp * Nk_pad * 3;   // 192 floats per 64-key block
+  const float* KCb = KC + (int64_t)kvp * Nk_pad * 2;   // 128 floats per 64-key block
 
   const int n_blocks = Nk_pad / BK;
   const int j_end = CAUSAL ? min(n_blocks, (qt * PP_BM + PP_BM - 1) / BK + 1) : n_blocks;
@@ -70,7 +70,7 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
 
   // ---- staging. K: wave w carries rows 8w..8w+7 (lane l: row 8w + l/8, chunk slot l%8 holding
   // logical chunk (l%8) ^ kswz(row)). V^T: rows 16w..16w+15 (lane l: row 16w + l/4, slot l%4
-  // holding (l%4) ^ vswz(d)). Constants: waves 0..2 carry floats 64w..64w+63 of 192.
+  // holding (l%4) ^ vswz(d)). Constants: waves 0 and 1 carry floats 64w..64w+63 of 128.
   const int krow = 8 * w + (lane >> 3), kpos = lane & 7;
   const uint32_t k_off = (uint32_t)(krow * HD + 16 * (kpos ^ kswz(krow)));
   const int vd = 16 * w + (lane >> 2), vpos = lane & 3;
@@ -85,7 +85,7 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
   auto dma_vc = [&](int j, int p) {
     const uint32_t base = lds0 + (uint32_t)p * (uint32_t)sizeof(StageBuf<HD>);
     dma16(Vb, v_off + (uint32_t)BK * (uint32_t)j, base + BK * HD);
-    if (w < 3) dma4(KCb, c_off + (uint32_t)(192 * 4) * (uint32_t)j, base + 2 * BK * HD - 768 * w);
+    if (w < 2) dma4(KCb, c_off + (uint32_t)(128 * 4) * (uint32_t)j, base + 2 * BK * HD - 768 * w);
   };
 
   dma_k(0, 0);

@@ -351,22 +351,19 @@ __global__ __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(QUANT_BLOCKS
           word = (u32x2){fp8x4(x[0], x[1], x[2], x[3]), fp8x4(x[4], x[5], x[6], x[7])};
         }
         *(u32x2*)(K8 + (bh * N_pad + n) * D + 8 * cg) = word;
-        // The main loop's per-key constants of 64-key block n/64 (KC, optional): SK, the fma
-        // addend -RN(1.5*2^23*SK) (0 for e4m3 K) and RN(SV'*448), 64 floats each.
-        float* kc = KC ? KC + (bh * (N_pad / 64) + n / 64) * 192 + (n & 63) : nullptr;
+        // The main loop's per-key constants of 64-key block n/64 (KC, optional): SK and
+        // RN(SV'*448), 64 floats each.
+        float* kc = KC ? KC + (bh * (N_pad / 64) + n / 64) * 128 + (n & 63) : nullptr;
         if (cg == 0) {
           const float ske = live ? sk : 1.0f;
           SK[bh * N_pad + n] = ske;
-          if (kc) {
-            kc[0] = ske;
-            kc[64] = KINT8 ? -(MAGIC_SEED * ske) : 0.0f;
-          }
+          if (kc) kc[0] = ske;
         }
         if (cg == 1) {
           const float sv = SV[bh * N_pad + n];
           const float svp = fold ? __fdiv_rn(sv, S) : sv;
           if (fold) SV[bh * N_pad + n] = svp;
-          if (kc) kc[128] = svp * P_SCALE;
+          if (kc) kc[64] = svp * P_SCALE;
         }
       }
     }

@@ -32,11 +32,6 @@ constexpr int NPAD = 64;         // N_pad granule
 constexpr float P_SCALE = 448.0f;
 constexpr float I8_MAX = 127.0f;
 constexpr float SCALE_FLOOR = 1e-12f;
-// 1.5 * 2^23: seeding an int32 MFMA accumulator with its bit pattern makes the result, read as
-// a float, 1.5*2^23 + (integer dot product) exactly. The prologue still writes -RN(1.5*2^23*SK) as
-// the middle row of the per-key constants (KCONST's layout); the main loops now zero-seed and
-// convert, and read only the SK and RN(SV'*448) rows.
-constexpr float MAGIC_SEED = 12582912.0f;
 constexpr float LOG2E_F = 1.4426950408889634f;
 
 // 16-bit element widen. bf16 -> fp32 and fp16 -> fp32 are exact.

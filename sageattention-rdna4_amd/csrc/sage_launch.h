@@ -36,7 +36,7 @@ struct PrologueArgs {
   float* mean;
   float* vmean;    // required with smooth_v: V's sequence mean (B*H, 128) fp32
   float* s;
-  float* kconst;   // optional: the main loop's per-key constants (B*H, N_pad/64, 3, 64) fp32
+  float* kconst;   // optional: the main loop's per-key constants (B*H, N_pad/64, 2, 64) fp32
   void* workspace;
 };
 hipError_t launch_prologue(const PrologueArgs& a, hipStream_t stream);

@@ -196,7 +196,7 @@ def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=
     el8, nf = BH_kv * n_pad * D, BH_kv * n_pad * 4
     ws_bytes = lib.workspace_bytes(BH_kv, N_kv)
     parts = [("k8", el8), ("sk", nf), ("v8t", el8), ("sv", nf), ("s", BH_kv * 4),
-             ("kconst", 3 * nf), ("ws", ws_bytes)]
+             ("kconst", 2 * nf), ("ws", ws_bytes)]
     if return_lse and smooth_k:
         parts.append(("kmean", BH_kv * D * 4))
     if smooth_v:

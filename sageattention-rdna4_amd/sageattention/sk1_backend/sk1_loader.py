@@ -183,7 +183,7 @@ class SageLib:
                     n_pad, kconst=None, smooth_v=False, vmean=None):
         """K/V prologue on logical (B, H, N, D) views `k`, `v`, D = 64 or 128 (see
         `sage_kv_prologue`).
-        `kconst` (optional) receives the main loop's per-key constants, (B*H, N_pad/64, 3, 64);
+        `kconst` (optional) receives the main loop's per-key constants, (B*H, N_pad/64, 2, 64);
         with `smooth_v`, `vmean` ((B*H, 128) fp32) receives V's sequence mean."""
         B, H, N, D = (int(x) for x in k.shape)
         rc = self.lib.sage_kv_prologue(

@@ -36,7 +36,7 @@ def _run_prologue(k, v, *, k_int8, smooth_k, fold, layout="HND", with_kconst=Fal
     mean = torch.full((BH, D), float("nan"), device=dev)
     vmean = torch.full((BH, D), float("nan"), device=dev)
     ws = torch.full((lib.workspace_bytes(BH, N),), 0xFF, device=dev, dtype=torch.uint8)
-    kc = (torch.full((BH, n_pad // 64, 3, 64), float("nan"), device=dev) if with_kconst
+    kc = (torch.full((BH, n_pad // 64, 2, 64), float("nan"), device=dev) if with_kconst
           else None)
     lib.kv_prologue(kk, vv, k8, sk, v8t, sv, s, mean, ws, k_int8=k_int8, smooth_k=smooth_k,
                     fold=fold, n_pad=n_pad, kconst=kc, smooth_v=smooth_v, vmean=vmean)
@@ -151,8 +151,8 @@ def test_prologue_strided_views_same_bits(dtype):
 @pytest.mark.parametrize("case", [CASES[3], CASES[4], CASES[9], CASES[10]], ids=lambda c: "%s-%s-N%d" % (
     str(c[0]).split(".")[-1], "i8" if c[1] else "f8", c[2]))
 def test_prologue_kconst_layout(case):
-    # The main loop's per-key constants: for each 64-key block, SK, -RN(1.5*2^23*SK) (int8 K; 0 for
-    # e4m3 K) and RN(SV'*448), each one fp32 rounding of the prologue's own SK / SV' bits.
+    # The main loop's per-key constants: for each 64-key block, SK and RN(SV'*448), the second one
+    # fp32 rounding of the prologue's own SV' bits.
     dtype, k_int8, N, H, off, outl, std = case
     q, k, v = make_qkv(1, H, N, seed=N + 7, dtype=dtype, std=std, k_offset_std=off,
                        outlier_frac=outl)
@@ -161,15 +161,12 @@ def test_prologue_kconst_layout(case):
     got = _run_prologue(k.cuda(), v.cuda(), k_int8=k_int8, smooth_k=True, fold=True,
                         with_kconst=True)
     BH, n_pad = H, oracle.n_pad_for(N)
-    kc = got["kconst"].reshape(BH, n_pad // 64, 3, 64)
+    kc = got["kconst"].reshape(BH, n_pad // 64, 2, 64)
     sk = got["sk"].reshape(BH, n_pad // 64, 64)
     svp = got["sv"].reshape(BH, n_pad // 64, 64)
-    magic = torch.tensor(12582912.0, dtype=torch.float32)
-    want_nsk = -(magic * sk) if k_int8 else torch.zeros_like(sk)
     want_w = svp * oracle.P_SCALE
     assert bytes_equal(kc[:, :, 0].contiguous(), sk), mismatch_report(kc[:, :, 0], sk, "kc.sk")
-    assert bytes_equal(kc[:, :, 1].contiguous(), want_nsk), mismatch_report(kc[:, :, 1], want_nsk, "kc.nsk")
-    assert bytes_equal(kc[:, :, 2].contiguous(), want_w), mismatch_report(kc[:, :, 2], want_w, "kc.w")
+    assert bytes_equal(kc[:, :, 1].contiguous(), want_w), mismatch_report(kc[:, :, 1], want_w, "kc.w")
     ref = _oracle_prologue(k, v, k_int8=k_int8, smooth_k=True)
     assert bytes_equal(got["sv"], ref["svp"])
 
@@ -243,10 +240,10 @@ def test_prologue_d64_bit_exact(case, smooth_k, smooth_v):
     for name, rname in (("k8", "k8"), ("sk", "sk"), ("v8t", "v8t"), ("sv", "svp"), ("s", "s")):
         assert bytes_equal(got[name], ref[rname]), mismatch_report(got[name], ref[rname], name)
     n_pad = oracle.n_pad_for(N)
-    kc = got["kconst"].reshape(H, n_pad // 64, 3, 64)
+    kc = got["kconst"].reshape(H, n_pad // 64, 2, 64)
     assert bytes_equal(kc[:, :, 0].contiguous(), got["sk"].reshape(H, n_pad // 64, 64))
     w = got["sv"].reshape(H, n_pad // 64, 64) * oracle.P_SCALE
-    assert bytes_equal(kc[:, :, 2].contiguous(), w)
+    assert bytes_equal(kc[:, :, 1].contiguous(), w)
 
 
 @pytest.mark.parametrize("dtype,qk_int8", [(torch.float16, True), (torch.float16, False),

@@ -26,7 +26,7 @@ def _outputs(BH, n_pad, D, k_int8, dev):
                 sk=fill((BH, n_pad), torch.float32), v8t=fill((BH, D, n_pad), torch.float8_e4m3fn),
                 sv=fill((BH, n_pad), torch.float32), s=fill((BH,), torch.float32),
                 mean=fill((BH, D), torch.float32), vmean=fill((BH, D), torch.float32),
-                kconst=fill((BH, n_pad // 64, 3, 64), torch.float32))
+                kconst=fill((BH, n_pad // 64, 2, 64), torch.float32))
 
 
 def _both(lib, k, v, *, k_int8, smooth_k, smooth_v):
