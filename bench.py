@@ -327,7 +327,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--kernel", type=int, default=0, choices=(0, 1, 2, 3),
-                    help="main-loop kernel: 0 by size (the library's default), 1 the 128-query "
+                    help="main-loop kernel: 0 the library's choice by grid fill, 1 the 128-query "
                          "kernel, 2 the 256-query ping-pong, 3 the pipelined 128-query kernel")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of the benchmark, run a plain device copy of this many MiB "

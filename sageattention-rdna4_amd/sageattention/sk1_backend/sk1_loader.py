@@ -249,7 +249,8 @@ class SageLib:
     def attn_fwd(self, q, k8, kconst, v8t, s, o, *, qk_int8, causal, sm_scale, n_pad, kernel=0,
                  lse=None, kmean=None, n_kv=None, vmean=None):
         """Main loop on logical (B, H, N, D) views `q`, `o` (see `sage_attn_fwd_ex`; `kernel`:
-        0 by size, 1 the 128-query kernel, 2 the 256-query ping-pong). The prologue outputs
+        0 the library's choice by grid fill, 1 the 128-query kernel, 2 the 256-query ping-pong,
+        3 the pipelined 128-query kernel). The prologue outputs
         `k8` (B*H_kv, n_pad, D) etc. give H_kv; `n_kv` is the key count (default N, and `n_pad`
         is then ceil(n_kv/64)*64). `lse` (optional, (B, H, N) fp32) receives each row's
         logsumexp; `kmean` ((B*H_kv, 128) fp32) adds its smooth_k correction; `vmean`
