@@ -87,3 +87,33 @@ def mismatch_report(a, b, name):
     idx = diff.nonzero()[:5].tolist()
     ex = [(i, a[tuple(i)].float().item(), b[tuple(i)].float().item()) for i in idx]
     return "%s: %d/%d differ, e.g. %s" % (name, n, diff.numel(), ex)
+
+
+def emulate_rows(q, k, v, rows, *, tensor_layout="HND", is_causal=False, smooth_k=True,
+                 smooth_v=False):
+    """The CPU emulation (`oracle.emulate_sageattn`) of the query rows in `rows` (a range) only, for
+    every plane: the prologue over the whole K/V planes, then the main loop's arithmetic for just
+    those rows (rows are independent). Returns `(o, lse)`: o (B, H, len(rows), D) in q's dtype
+    (HND order whatever the layout), lse (B, H, len(rows)) fp32."""
+    import oracle
+    qq, kk, vv = (oracle.to_hnd(t, tensor_layout) for t in (q, k, v))
+    B, H, N, D = qq.shape
+    H_kv, N_kv = kk.shape[1], kk.shape[2]
+    kvp = oracle.kv_planes(B, H, H_kv, N, N_kv, is_causal)
+    qk_int8 = q.dtype == torch.float16
+    sm = float(D ** -0.5)
+    n_pad = oracle.n_pad_for(N_kv)
+    kr, vr = (t.reshape(B * H_kv, N_kv, D) for t in (kk, vv))
+    mean = oracle.kseq_mean(kr) if smooth_k else None
+    k8, sk = oracle.quant_k(kr, n_pad, mean=mean, int8=qk_int8)
+    vmean = oracle.kseq_mean(vr) if smooth_v else None
+    v8t, sv = oracle.quant_v(vr, n_pad, mean=vmean)
+    s, svp = oracle.fold_v_scale(sv)
+    qr = qq.reshape(B * H, N, D)[:, rows.start:rows.stop]
+    q8, _, c_q = oracle.quant_q(qr, sm, int8=qk_int8)
+    lse2 = torch.empty(B * H, len(rows), dtype=torch.float32)
+    o = oracle.attention_tiles(q8, c_q, k8[kvp], sk[kvp], v8t[kvp], svp[kvp], s[kvp], N_kv,
+                               is_causal, q.dtype, row0=rows.start, lse_out=lse2,
+                               vmean=None if vmean is None else vmean[kvp])
+    lse = oracle.row_lse(lse2, qr, None if mean is None else mean[kvp], sm)
+    return o.view(B, H, len(rows), D), lse.view(B, H, len(rows))

@@ -644,3 +644,21 @@ def test_row_subset_equals_the_full_emulation(causal):
         q8, _, cq = oracle.quant_q(q[0][:, r0:r1], 128 ** -0.5, int8=True)
         part = oracle.attention_tiles(q8, cq, k8, sk, v8t, svp, s, N, causal, q.dtype, row0=r0)
         assert torch.equal(part[0], full[r0:r1]), (r0, r1)
+
+
+@pytest.mark.parametrize("causal,smooth_v,layout", [(True, False, "HND"), (False, True, "NHD")])
+def test_emulate_rows_equals_the_full_emulation(causal, smooth_v, layout):
+    """The row-slice emulation used by the large GPU sweep gives the full emulation's rows and
+    logsumexp bit for bit, with grouped K/V heads, a key length of their own and smooth_v."""
+    from sage_testutil import emulate_rows
+    N = 200
+    q, k, v = make_qkv(2, 4, N, seed=5, k_offset_std=2.0, layout=layout, h_kv=2,
+                       n_kv=N if causal else 150, v_offset_std=1.0)
+    full = oracle.emulate_sageattn(q, k, v, tensor_layout=layout, is_causal=causal,
+                                   smooth_v=smooth_v)
+    o_full = oracle.to_hnd(full["o"], layout)
+    for r in (range(0, 64), range(70, 133), range(N - 64, N)):
+        o, lse = emulate_rows(q, k, v, r, tensor_layout=layout, is_causal=causal,
+                              smooth_v=smooth_v)
+        assert torch.equal(o, o_full[:, :, r.start:r.stop]), r
+        assert torch.equal(lse, full["lse"][:, :, r.start:r.stop]), r
