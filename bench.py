@@ -10,7 +10,8 @@ causal (the reference's `bench/bench_attention.py:140`).
 The method follows the reference's (`docs/METHOD.md:14-45`, `bench/bench_attention.py:49-58`):
 1. W untimed warm-up calls, then an untimed clock-settling phase by time: at least `--settle`
    seconds (default 4) and 40 calls, continued in half-second chunks while the shader clock still
-   rises (at most 10 s). Recorded as `settle` (calls, seconds, the clock readings).
+   rises (at most 10 s). Recorded as `settle` (calls, seconds, the clock readings, and the board
+   power and power cap at its end, `board_power`: the card lowers its clock to hold the cap).
 2. The timed region: exactly K calls of the public `sageattn(...)` (with `--kernel` other than 0,
    of `sk1_forward` with that kernel), bracketed by device synchronizations, with the shader
    clock read before and after. `ms_per_step` and `value` come from it.
@@ -211,6 +212,27 @@ def sclk_mhz():
     return None
 
 
+def board_power(root="/sys/class/drm"):
+    """The board's power draw and power cap in W, read from sysfs hwmon (`power1_average`, else
+    `power1_input`; `power1_cap`; microwatts): plain file reads. None for what is unreadable; with
+    several AMD cards, the first one that reports a power draw."""
+    import glob
+
+    def read_w(path):
+        try:
+            with open(path) as f:
+                return int(f.read().strip()) / 1e6
+        except (OSError, ValueError):
+            return None
+    for d in sorted(glob.glob(os.path.join(root, "card*", "device", "hwmon", "hwmon*"))):
+        draw = read_w(os.path.join(d, "power1_average"))
+        if draw is None:
+            draw = read_w(os.path.join(d, "power1_input"))
+        if draw is not None:
+            return {"watts": round(draw, 1), "cap_watts": read_w(os.path.join(d, "power1_cap"))}
+    return None
+
+
 def settle(call, sync, *, min_calls=40, min_s=4.0, max_s=10.0, chunk_s=0.5, max_calls=20000,
            clock=None, now=time.perf_counter):
     """Untimed clock settling by time, not by call count (the reference's rule,
@@ -369,6 +391,8 @@ def main():
         call()
     sync()
     st = settle(call, sync, min_s=args.settle) if args.settle > 0 else None
+    if st is not None:
+        st["board_power"] = board_power()
     log("settle:", st)
 
     # the timed region: exactly K calls

@@ -154,3 +154,19 @@ def test_aa_twin_interleaves_and_reports_medians(bench):
     for k in ("range_a", "range_b"):
         lo, hi = aa[k]
         assert lo <= hi and lo <= aa["ms_" + k[-1]] <= hi
+
+
+def test_board_power_reads_hwmon(bench, tmp_path):
+    # power1_average in microwatts, else power1_input; the cap beside it; the first card with a
+    # power reading wins
+    h0 = tmp_path / "card0" / "device" / "hwmon" / "hwmon2"
+    h0.mkdir(parents=True)
+    (h0 / "temp1_input").write_text("50000\n")
+    h1 = tmp_path / "card1" / "device" / "hwmon" / "hwmon5"
+    h1.mkdir(parents=True)
+    (h1 / "power1_input").write_text("1331500000\n")
+    (h1 / "power1_cap").write_text("1400000000\n")
+    assert bench.board_power(str(tmp_path)) == {"watts": 1331.5, "cap_watts": 1400.0}
+    (h1 / "power1_average").write_text("1200000000\n")
+    assert bench.board_power(str(tmp_path))["watts"] == 1200.0
+    assert bench.board_power(str(tmp_path / "nothing")) is None
