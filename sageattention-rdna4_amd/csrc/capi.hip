@@ -143,14 +143,17 @@ double est_q128(int64_t blocks, int64_t cus) {
   }
   return t;
 }
-double est_q256(int64_t blocks, int64_t cus) { return (double)((blocks + cus - 1) / cus) * 2.0 / 1.75; }
+double est_q256(int64_t blocks, int64_t cus) {
+  return (double)((blocks + cus - 1) / cus) * 2.0 / 1.75;
+}
 
 int kernel_for(int64_t B, int64_t H, int64_t N, int64_t D, int causal, int64_t cus) {
   if (D != 128) return SAGE_KERNEL_PIPE;
   const int64_t nb256 = B * H * ((N + 255) / 256);
   if (causal) return nb256 >= 4 * cus ? SAGE_KERNEL_Q256 : SAGE_KERNEL_PIPE;
   const int64_t nb128 = B * H * ((N + 127) / 128);
-  return est_q256(nb256, cus) < 0.97 * est_q128(nb128, cus) ? SAGE_KERNEL_Q256 : SAGE_KERNEL_PIPE;
+  return est_q256(nb256, cus) < 0.97 * est_q128(nb128, cus) ? SAGE_KERNEL_Q256
+                                                              : SAGE_KERNEL_PIPE;
 }
 
 }  // namespace
@@ -161,14 +164,14 @@ int sage_attn_kernel_choice(int64_t B, int64_t H, int64_t N, int64_t D, int caus
   if (B < 1 || H < 1 || N < 1)
     return -fail(SAGE_ERR_INVALID, "shape: B, H and N must be positive (B=%lld H=%lld N=%lld)",
                  (long long)B, (long long)H, (long long)N);
-  if (D != 64 && D != 128) return -fail(SAGE_ERR_INVALID, "head_dim: %lld is not 64 or 128", (long long)D);
+  if (D != 64 && D != 128)
+    return -fail(SAGE_ERR_INVALID, "head_dim: %lld is not 64 or 128", (long long)D);
   if (cus <= 0) {
     const int rc = cus_of_current_device(&cus);
     if (rc) return -rc;
   }
   return kernel_for(B, H, N, D, causal, cus);
 }
-
 
 int sage_version(void) { return 100; }
 
