@@ -277,14 +277,14 @@ __device__ __forceinline__ KeyConsts load_key_consts(const ScaleTile& sc, int la
 struct BlockShift {
   float mc, alpha;
 };
-template <bool QK_INT8, bool CAUSAL>
+template <bool QK_INT8, bool CAUSAL, int NCONV = 0>
 __device__ __forceinline__ BlockShift scores_block(f32x16 (&sx)[2], float sk0, float sk1, int j, int q0,
                                                    int qrow, int N, int hh, float cq, float& m_x,
                                                    float& mc) {
   static_for<0, 32>([&](auto ic) {
     constexpr int jj = decltype(ic)::value;
     const float v = sx[jj >> 4][jj & 15];
-    const float d = QK_INT8 ? (float)__float_as_int(v) : v;
+    const float d = (QK_INT8 && jj >= NCONV) ? (float)__float_as_int(v) : v;
     sx[jj >> 4][jj & 15] = d * row_bcast<jj & 15>(jj < 16 ? sk0 : sk1);
   });
   const bool need_mask = CAUSAL ? (BK * j + BK - 1 > q0) : (BK * j + BK > N);
@@ -318,6 +318,17 @@ __device__ __forceinline__ BlockShift scores_block(f32x16 (&sx)[2], float sk0, f
   m_x = m_new;
   mc = mc_new;
   return {mc_new, alpha};
+}
+
+// int8 Q.K: the first NCONV of this lane's 32 raw int32 scores converted to fp32 in place (exact:
+// |Q8.K8| <= 2^21), so that a scores_block<..., NCONV> that follows skips their conversion. Lets a
+// kernel move the conversion out of the softmax's issue-bound stretch.
+template <int NCONV>
+__device__ __forceinline__ void convert_scores(f32x16 (&sx)[2]) {
+  static_for<0, NCONV>([&](auto ic) {
+    constexpr int jj = decltype(ic)::value;
+    sx[jj >> 4][jj & 15] = (float)__float_as_int(sx[jj >> 4][jj & 15]);
+  });
 }
 
 // O *= alpha before the block's P.V, skipped when every lane of the wave has alpha == 1.

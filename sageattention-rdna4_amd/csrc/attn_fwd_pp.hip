@@ -30,6 +30,12 @@ namespace sage {
 
 constexpr int PP_BM = 256;    // queries per block
 constexpr int PP_T = 512;     // threads per block
+#ifndef PP_NCONV_DEF
+#define PP_NCONV_DEF 16
+#endif
+// int8 Q.K: scores of the next block converted to fp32 at the end of the wave's MFMA phase (which
+// has slack) instead of in its softmax phase (issue-bound)
+constexpr int PP_NCONV = PP_NCONV_DEF;
 
 template <typename T, bool QK_INT8, bool CAUSAL>
 __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_pp_kernel(
@@ -165,7 +171,8 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
   auto softmax = [&](const int j) {
     __builtin_amdgcn_s_setprio(1);
     const BlockShift sh =
-        scores_block<QK_INT8, CAUSAL>(st, kcp.sk0, kcp.sk1, j, q0, qrow, Nk, hh, cq, m_x, mc);
+        scores_block<QK_INT8, CAUSAL, QK_INT8 ? PP_NCONV : 0>(st, kcp.sk0, kcp.sk1, j, q0, qrow, Nk,
+                                                             hh, cq, m_x, mc);
     probs_block<false>(st, kcp.w0, kcp.w1, cq, sh, l_i, acc, pb);
     alpha_pend = sh.alpha;
     __builtin_amdgcn_s_setprio(0);
@@ -173,6 +180,15 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
   // A phase's products are pinned before its barrier: without the pins the compiler is free to
   // sink MFMAs (which touch no memory) past the barrier into the next phase.
   auto pin_st = [&]() { asm volatile("" ::"v"(st[0]), "v"(st[1])); };
+  // (after the phase's last MFMAs: the scheduling barrier keeps the conversions from being hoisted
+  // above them, closer to the Q.K MFMAs whose results they read)
+  auto preconvert = [&]() {
+    if constexpr (QK_INT8) {
+      __builtin_amdgcn_sched_barrier(0);
+      convert_scores<PP_NCONV>(st);
+      pin_st();
+    }
+  };
   auto pin_pb = [&]() { asm volatile("" ::"v"(pb)); };
   auto end_phase1 = [&](bool more2) {
     __builtin_amdgcn_sched_barrier(0);
@@ -198,6 +214,7 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
     qk(I0{});
     pin_st();
     mfma_result_fence();
+    preconvert();
     prefetch_consts(I0{});
     auto blk = [&](const int jj, auto par) {
       constexpr int P = decltype(par)::value;
@@ -217,6 +234,7 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
       pv(par);
       pin_acc();
       pin_st();
+      preconvert();
       end_phase2();
     };
     for (j = 0; j + 3 <= w_end; j += 3) {
@@ -248,6 +266,7 @@ __global__ __launch_bounds__(PP_T) __attribute__((amdgpu_waves_per_eu(2, 2))) vo
         pin_st();
         mfma_result_fence();   // no P.V behind S^T in the first block
       }
+      preconvert();
       end_phase1(more2);
       if (more2) dma_vc(jj + 2, PF);
       softmax(jj);
