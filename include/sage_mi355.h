@@ -197,8 +197,9 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal,
  *   cus  compute units to plan for; <= 0: those of the current device (a device query)
  * head_dim 64 runs the pipelined kernel. At 128 the 256-query ping-pong runs when, on `cus` CUs,
  * its grid is estimated to finish at least 3 % sooner: a causal grid with at least 4 of its
- * blocks per CU; a non-causal one by whole rounds of blocks (up to three 128-query blocks or one
- * 256-query block resident per CU) at per-CU throughputs measured on MI355X.
+ * blocks per CU, unless padding the last query tile to 256 rows costs over 2 % more of the causal
+ * work than padding it to 128; a non-causal one by whole rounds of blocks (up to three 128-query
+ * blocks or one 256-query block resident per CU) at per-CU throughputs measured on MI355X.
  * Returns the kernel code, or -SAGE_ERR_INVALID for a bad shape or head_dim, or -SAGE_ERR_HIP
  * when the device query fails.
  */

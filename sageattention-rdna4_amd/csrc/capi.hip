@@ -147,10 +147,19 @@ double est_q256(int64_t blocks, int64_t cus) {
   return (double)((blocks + cus - 1) / cus) * 2.0 / 1.75;
 }
 
+// Causal: the padded rows of a plane's last query tile are its longest rows, so padding to
+// `tile` rows adds about 2 * pad / N of the plane's causal work.
+double causal_pad_work(int64_t N, int64_t tile) {
+  return 2.0 * (double)((N + tile - 1) / tile * tile - N) / (double)N;
+}
+
 int kernel_for(int64_t B, int64_t H, int64_t N, int64_t D, int causal, int64_t cus) {
   if (D != 128) return SAGE_KERNEL_PIPE;
   const int64_t nb256 = B * H * ((N + 255) / 256);
-  if (causal) return nb256 >= 4 * cus ? SAGE_KERNEL_Q256 : SAGE_KERNEL_PIPE;
+  if (causal)
+    return (nb256 >= 4 * cus && causal_pad_work(N, 256) - causal_pad_work(N, 128) < 0.02)
+               ? SAGE_KERNEL_Q256
+               : SAGE_KERNEL_PIPE;
   const int64_t nb128 = B * H * ((N + 127) / 128);
   return est_q256(nb256, cus) < 0.97 * est_q128(nb128, cus) ? SAGE_KERNEL_Q256
                                                               : SAGE_KERNEL_PIPE;

@@ -59,6 +59,9 @@ def test_kernel_choice_by_grid_fill():
         (1, 48, 4096, 128, True, PIPE),     # 768 blocks < 1024
         (1, 8, 32768, 128, True, Q256),     # exactly 1024 blocks
         (1, 8, 32512, 128, True, PIPE),     # 1016 blocks
+        (1, 48, 8771, 128, True, PIPE),     # 1680 blocks, but the last tile pads 189 of 256 rows:
+                                            # 2*189/8771 = 4.3 % more causal work, 1.4 % at 128
+        (1, 48, 47520, 128, True, Q256),    # pads 96 rows: 0.4 % against 0.1 %
         # non-causal, in units of one 128-query block alone on a CU:
         (1, 48, 1024, 128, False, Q256),    # 384 blocks: two on half the CUs, 2/1.52 = 1.32;
                                             # 192 blocks of 256 in one round: 2/1.75 = 1.14
