@@ -22,10 +22,11 @@ Reference files (paths relative to the reference repository root):
 * `sageattention/sk1_backend/quant_triton.py` -- the reference's fp32 sequence mean of its own
   smooth_v path (`vseq_mean_fp32_chunked`).
 
-Parity status: every function here is pinned by `tests/test_oracle.py` and the golden fixtures,
-except `vseq_mean_fp32_chunked`, whose order inside one 16-row Triton reduction the reference does
-not fix: **parity unpinned** at the bit level for it (pinned on integer-valued rows, by a scalar
-brute force of the stated order, and against the fp64 mean within the fp32 summation bound).
+Parity status: every function here is pinned by `tests/test_oracle.py` and the golden fixtures.
+For `vseq_mean_fp32_chunked` the pin covers everything the reference fixes (fp32 accumulation of
+16-row group sums in row order per 1024-row chunk, chunk partials in chunk order, one fp32
+division), on data where that accumulation must round; the order inside one 16-row Triton
+`tl.sum` is not fixed by the reference and is taken as a pairwise tree.
 """
 import math
 
@@ -80,8 +81,9 @@ def vseq_mean_fp32_chunked(x, chunk=1024, group=16):
     read as 0). Stage 2 (`_kseq_finalize_mean`, `:334-343`): the chunk partials summed in chunk order
     in fp32, then one fp32 division by N. The order inside one 16-row `tl.sum` is Triton's
     reduction tree, which the reference does not fix; it is taken here as a balanced pairwise tree
-    (rows 0+1, 2+3, ..., then pairs of pairs). So this restatement is the reference's definition up
-    to that order: parity at the bit level is unpinned, and it is used only at tolerance level.
+    (rows 0+1, 2+3, ..., then pairs of pairs). Where each group's sum is exact in fp32 (every
+    order then agrees), this is the reference's function bit for bit; the tests pin it there
+    against an exact rational simulation, with the rounding the fp32 accumulation forces.
     `x`: (BH, N, D) fp16/bf16. Returns (BH, D) fp32.
     """
     BH, N, D = x.shape

@@ -534,6 +534,97 @@ def test_reference_fp32_chunked_mean_order_by_brute_force():
         assert f32_bits(got[0, d].item()) == f32_bits(float(np.float32(tot / np.float32(70))))
 
 
+def _fp32_chunked_mean_exact(x, chunk=1024, group=16, chunk_order=1, divide="div"):
+    """The reference's fp32 chunked mean (`quant_triton.py:303-343`) in exact rational arithmetic,
+    each fp32 operation one `rn32`: per chunk of `chunk` rows an accumulator starting at 0 receives
+    the `group`-row sums in row order, the chunk partials are added in chunk order (reversed with
+    `chunk_order=-1`), then one division by N. Group sums are formed exactly and rounded once,
+    which is every order's result when, as on `_exact_group_data`, each one is representable.
+    `divide`: "div" (the reference), "recip" (times RN(1/N)), "pad" (by the padded length), "f64"
+    (the fp32 sum divided in fp64, then rounded to fp32)."""
+    N, D = x.shape
+    out = []
+    for c in range(D):
+        col = [Fraction(float(v)) for v in x[:, c]]
+        parts = []
+        for c0 in range(0, N, chunk):
+            acc = Fraction(0)
+            for g0 in range(c0, c0 + chunk, group):
+                gs = sum(col[g0:min(g0 + group, N)], Fraction(0)) if g0 < N else Fraction(0)
+                acc = Fraction(rn32(acc + Fraction(rn32(gs))))
+            parts.append(acc)
+        tot = Fraction(0)
+        for p_ in parts[::chunk_order]:
+            tot = Fraction(rn32(tot + p_))
+        if divide == "f64":
+            out.append(float(np.float32(np.float64(float(tot)) / np.float64(N))))
+            continue
+        den = {"div": Fraction(N), "pad": Fraction(len(parts) * chunk)}.get(divide)
+        out.append(rn32(tot / den) if den is not None
+                   else rn32(tot * Fraction(rn32(Fraction(1, N)))))
+    return out
+
+
+def _exact_group_data(seed, N, D):
+    """fp16 columns whose every 16-row group is all zeros, all one value with at most 3 significant
+    bits (1024 .. 3584, either sign), or a single nonzero row 1 + k/1024 (k odd): every partial sum
+    inside a group, in any order, is exact in fp32, so Triton's unspecified order inside one
+    `tl.sum` cannot change a bit, while the fp32 `acc +=` across groups (magnitudes up to ~2^21
+    against fine bits at 2^-10) and across chunks must round."""
+    rng = np.random.default_rng(seed)
+    x = np.zeros((N, D), dtype=np.float16)
+    for c in range(D):
+        for g0 in range(0, N, 16):
+            kind = rng.integers(0, 3)
+            if kind == 1:
+                x[g0:g0 + 16, c] = float(rng.choice([1024., 1536., 2048., 3072., 3584.])) \
+                    * float(rng.choice([-1, 1]))
+            elif kind == 2:
+                r = g0 + int(rng.integers(0, 16))
+                if r < N:
+                    x[r, c] = (1 + (2 * int(rng.integers(0, 512)) + 1) / 1024.0) \
+                        * float(rng.choice([-1, 1]))
+    for c in range(D):
+        for g0 in range(0, N, 16):
+            vals = {float(v) for v in x[g0:g0 + 16, c] if v != 0}
+            assert len(vals) <= 1
+            for v in vals:
+                assert all(rn32(k * Fraction(v)) == k * Fraction(v) for k in range(17))
+    return x
+
+
+def test_reference_fp32_chunked_mean_pinned_where_fp32_rounding_decides():
+    # The part of the reference's mean the reference fixes -- fp32 accumulation of 16-row group
+    # sums in row order within 1024-row chunks, chunk partials in chunk order, one fp32 division
+    # (quant_triton.py:303-343) -- on data where that accumulation must round and the order
+    # inside a group cannot matter (three chunks, a ragged last chunk and group). The oracle must
+    # equal the exact simulation bit for bit, and each plausible slip must be caught.
+    N, D = 2599, 16
+    x = _exact_group_data(7, N, D)
+    want = _fp32_chunked_mean_exact(x)
+    got = oracle.vseq_mean_fp32_chunked(torch.from_numpy(x)[None])[0].tolist()
+    assert [f32_bits(a) for a in got] == [f32_bits(a) for a in want]
+
+    def caught(other):
+        return sum(f32_bits(a) != f32_bits(b) for a, b in zip(want, other))
+    xt = torch.from_numpy(x)
+    # fp64 accumulation (the whole sum in fp64, or in fp64 per chunk), one rounding at the end
+    assert caught((xt.double().sum(0) / N).float().tolist()) > 0
+    per_chunk64 = sum(xt[c0:c0 + 1024].double().sum(0) for c0 in range(0, N, 1024))
+    assert caught((per_chunk64 / N).float().tolist()) > 0
+    assert caught([rn32(Fraction(math.fsum(float(v) for v in x[:, c])) / N)
+                   for c in range(D)]) > 0
+    assert caught(_fp32_chunked_mean_exact(x, chunk_order=-1)) > 0     # partials in another order
+    assert caught(_fp32_chunked_mean_exact(x, chunk=512)) > 0          # another chunk length
+    assert caught(_fp32_chunked_mean_exact(x, group=32)) > 0           # another group length
+    assert caught(_fp32_chunked_mean_exact(x, divide="recip")) > 0     # times RN(1/N)
+    assert caught(_fp32_chunked_mean_exact(x, divide="pad")) > 0       # by the padded length
+    # The division done in fp64 and rounded to fp32 is not a slip: for fp32 operands it gives the
+    # same bits as the fp32 division (double rounding is innocuous for +, -, *, / when the wider
+    # format has at least 2p + 2 significand bits, 53 >= 2*24 + 2; Figueroa 1995), as here.
+    assert caught(_fp32_chunked_mean_exact(x, divide="f64")) == 0
+
+
 def test_fp64_mean_is_within_a_few_ulps_of_the_reference_fp32_mean():
     # the build's V mean (fp64 sums, one rounding) against the reference's fp32 chunked mean on
     # offset fp16 data at a long length: their difference is the fp32 summation error alone,
