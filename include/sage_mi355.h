@@ -41,7 +41,9 @@ extern "C" {
 #define SAGE_KERNEL_Q256 2  /* 256 queries per block of 8 waves, two groups in ping-pong */
 #define SAGE_KERNEL_PIPE 3  /* 128 queries per block of 4 waves, MFMAs pipelined inside each wave */
 
-/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH: 200 (0.2.0). 0.2.0 changed KCONST from
+ * three rows per 64-key block to the two above; a caller built against 0.1.0 (100) that allocates
+ * or fills KCONST itself must check for 200. */
 int sage_version(void);
 
 /* Text of the last error on the calling thread ("" if none). Valid until the next call. */
@@ -141,8 +143,8 @@ int sage_kv_prologue_noalloc(int dtype, int k_int8, int smooth_k, int smooth_v, 
  * (`kernels/hip/sk1_t6in.hip:323-332`) and `sk1t4a1{sb,nb}_attn_fwd_c{0,1}`
  * (`kernels/hip/sk1_t4a1sb.hip:300-308`). Q is quantized per row inside the kernel (int8 when
  * qk_int8, else fp8 e4m3). The reference's SK and SV' inputs arrive as `kconst`, the prologue's
- * per-key constants (SK, -RN(1.5*2^23*SK), RN(SV'*448) per 64-key block, written from the folded
- * SV'); `s` is the fold S.
+ * per-key constants (two rows of 64 fp32 per 64-key block: SK, then RN(SV'*448), written from
+ * the folded SV'); `s` is the fold S.
  *
  *   q, o   logical (B, H, N, 128) views of `dtype`, element strides (q_sb, q_sh, q_sr) / (o_...)
  *   k8, kconst, v8t, s   the prologue's outputs for the same B, H, N, N_pad and qk_int8

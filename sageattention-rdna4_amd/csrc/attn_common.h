@@ -194,9 +194,8 @@ __device__ __forceinline__ void qk_block(const u8* __restrict__ kbuf, const QFra
   }
 }
 
-// Per-key constants of one 64-key block in LDS, in the layout the prologue writes them (768
-// bytes/block): SK, -RN(1.5*2^23*SK) (0 for the fp8 Q.K form; staged but not read by the main
-// loops, which convert the zero-seeded int32 dot product instead) and RN(SV' * 448).
+// Per-key constants of one 64-key block in LDS, in the layout the prologue writes them (two rows
+// of 64 fp32, 512 bytes per block): SK, then W = RN(SV' * 448).
 struct ScaleTile {
   float sk[BK];
   float w[BK];

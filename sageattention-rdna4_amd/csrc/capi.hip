@@ -57,13 +57,39 @@ int check_shape(int64_t B, int64_t H, int64_t N, int64_t N_pad) {
   if (N_pad < N || (N_pad % 64) != 0)
     return fail(SAGE_ERR_INVALID, "n_pad: N_pad must be a multiple of 64 and >= N (N=%lld N_pad=%lld)",
                 (long long)N, (long long)N_pad);
-  // Grids are 1-D lists of (plane, tile) blocks, so B*H itself has no limit of its own; the
-  // 128-row tiles of every plane must fit one int32 block index, and a plane's padded rows the
-  // 32-bit in-plane offsets of the main loop's staging.
-  if (N_pad > kInt32Max / 128 || B * H * ((N + 127) / 128) > kInt32Max)
-    return fail(SAGE_ERR_INVALID, "shape too large for the grid (B*H=%lld N=%lld)",
-                (long long)(B * H), (long long)N);
+  // A plane's padded rows must fit the 32-bit in-plane offsets of the main loop's staging; the
+  // grids themselves are bounded per launch (check_grid).
+  if (N_pad > kInt32Max / 128 || B > kInt32Max || H > kInt32Max || B * H > kInt32Max)
+    return fail(SAGE_ERR_INVALID, "grid: shape too large (B*H=%lld N=%lld)", (long long)(B * H),
+                (long long)N);
   return SAGE_OK;
+}
+
+// Every grid is a 1-D list of blocks, so B*H has no limit of its own; HIP bounds one launch at
+// 2^32 - 1 threads (blocks times threads per block).
+int check_grid(const char* what, int64_t blocks, int64_t threads) {
+  if (blocks < 1 || blocks > (int64_t)(0xFFFFFFFFull / (uint64_t)threads))
+    return fail(SAGE_ERR_INVALID,
+                "grid: %s needs %lld blocks of %lld threads, beyond HIP's 2^32-1 threads per launch",
+                what, (long long)blocks, (long long)threads);
+  return SAGE_OK;
+}
+
+// The main-loop grids: 128-query blocks of 256 threads (SAGE_KERNEL_Q128, SAGE_KERNEL_PIPE) and
+// 256-query blocks of 512 threads (SAGE_KERNEL_Q256). Checked for every kernel, so the refusal
+// does not depend on the automatic choice.
+int check_main_grid(int64_t B, int64_t H, int64_t N) {
+  int rc = check_grid("the 128-query main loop", B * H * ((N + 127) / 128), 256);
+  if (rc) return rc;
+  return check_grid("the 256-query main loop", B * H * ((N + 255) / 256), 512);
+}
+
+// The prologue's two passes: C1 and C2 blocks per plane of 256 threads.
+int check_prologue_grid(int64_t BH, int64_t N, int64_t N_pad) {
+  const sage::PrologueGeom g = sage::prologue_geom(BH, N, N_pad);
+  const int64_t c = g.C1 > g.C2 ? g.C1 : g.C2;
+  if (c > kInt32Max / BH) return check_grid("the prologue", kInt32Max, 256);
+  return check_grid("the prologue", c * BH, 256);
 }
 
 int check_head_dim(int64_t D) {
@@ -182,7 +208,7 @@ int sage_attn_kernel_choice(int64_t B, int64_t H, int64_t N, int64_t D, int caus
   return kernel_for(B, H, N, D, causal, cus);
 }
 
-int sage_version(void) { return 100; }
+int sage_version(void) { return 200; }
 
 #ifndef SAGE_BUILD_ID
 #define SAGE_BUILD_ID "unknown"
@@ -209,6 +235,7 @@ int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int smooth_v, int fold
     return fail(SAGE_ERR_INVALID, "bf16_int8: int8 K is served for fp16 inputs only");
   int rc = check_shape(B, H, N, N_pad);
   if (rc) return rc;
+  if ((rc = check_prologue_grid(B * H, N, N_pad))) return rc;
   if ((rc = check_head_dim(D))) return rc;
   if ((rc = check_view("k", k, k_sb, k_sh, k_sr))) return rc;
   if ((rc = check_view("v", v, v_sb, v_sh, v_sr))) return rc;
@@ -285,6 +312,7 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
     return fail(SAGE_ERR_INVALID, "bf16_int8: int8 Q.K is served for fp16 inputs only");
   int rc = check_shape(B, H, N, (N + 63) / 64 * 64);
   if (rc) return rc;
+  if ((rc = check_main_grid(B, H, N))) return rc;
   if (H_kv < 1 || H % H_kv != 0)
     return fail(SAGE_ERR_INVALID, "heads: H (%lld) must be a multiple of H_kv (%lld)",
                 (long long)H, (long long)H_kv);
@@ -368,6 +396,7 @@ int sage_attn_fwd_sk(int dtype, int qk_int8, int causal, const void* q, int64_t 
     return fail(SAGE_ERR_INVALID, "bf16_int8: int8 Q.K is served for fp16 inputs only");
   int rc = check_shape(B, H, N, (N + 63) / 64 * 64);
   if (rc) return rc;
+  if ((rc = check_main_grid(B, H, N))) return rc;
   if (H_kv < 1 || H % H_kv != 0)
     return fail(SAGE_ERR_INVALID, "heads: H (%lld) must be a multiple of H_kv (%lld)",
                 (long long)H, (long long)H_kv);
@@ -430,6 +459,7 @@ int sage_kseq_mean(int dtype, const void* k, int64_t k_sb, int64_t k_sh, int64_t
   const int64_t N_pad = (N + 63) / 64 * 64;
   int rc = check_shape(B, H, N, N_pad);
   if (rc) return rc;
+  if ((rc = check_prologue_grid(B * H, N, N_pad))) return rc;
   if (D != 64 && D != 128)
     return fail(SAGE_ERR_INVALID, "mean_head_dim: D must be 64 or 128 (got %lld)", (long long)D);
   if ((rc = check_view("k", k, k_sb, k_sh, k_sr))) return rc;
@@ -473,9 +503,7 @@ int sage_quant_q(int dtype, int qk_int8, const void* q, int64_t q_sb, int64_t q_
     return fail(SAGE_ERR_INVALID, "bf16_int8: int8 Q is served for fp16 inputs only");
   int rc = check_shape(B, H, N, (N + 63) / 64 * 64);
   if (rc) return rc;
-  if (B * H * ((N + 31) / 32) > kInt32Max)
-    return fail(SAGE_ERR_INVALID, "shape too large for the grid (B*H=%lld N=%lld)",
-                (long long)(B * H), (long long)N);
+  if ((rc = check_grid("the Q quantizer", B * H * ((N + 31) / 32), 64))) return rc;
   if ((rc = check_head_dim(D))) return rc;
   if ((rc = check_view("q", q, q_sb, q_sh, q_sr))) return rc;
   if (!q8 || !sq || !cq) return fail(SAGE_ERR_INVALID, "an output pointer is NULL");

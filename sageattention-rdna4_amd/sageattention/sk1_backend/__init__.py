@@ -36,7 +36,8 @@ ENVELOPE = dict(
     contiguous="any view strided_view_reason accepts",
     causal=(0, 1),
     smooth_k=(False, True),
-    batch_heads="any",
+    batch_heads=("any B*H whose grids fit HIP's 2^32-1 threads per launch: "
+                 "B*H*ceil(N/128) < 2^24, B*H*ceil(N/256) < 2^23, B*H < 2^24"),
     heads="H_kv divides H (grouped-query / multi-query K/V heads)",
     seq_len="N >= 1, N_kv >= 1; N == N_kv when causal",
     return_lse=(False, True),

@@ -88,7 +88,7 @@ def test_library_host_calls_without_a_gpu():
     if not os.path.isfile(sk1_loader.LIB_PATH):
         pytest.skip("library not built")
     L = sk1_loader.SageLib.get()
-    assert L.version >= 100
+    assert L.version == 200
     assert L.workspace_bytes(48, 47520) > 48 * 128 * 8
     assert L.workspace_bytes(1, 1) > 0
     i64 = ctypes.c_int64
@@ -124,18 +124,16 @@ def test_library_host_calls_without_a_gpu():
     rc = L.lib.sage_quant_q(0, 1, p16, 12800, 12800, 128, 1, 1, 100, 32, ctypes.c_float(0.1),
                             p16, p16, p16, None)
     assert rc == 1 and b"head_dim" in L.lib.sage_last_error()
-    # the workspace size depends on B*H and N only: a larger N_pad than ceil(N/64)*64 passes the
-    # size check with workspace_bytes(B*H, N) (the call then fails only at the launch, no GPU)
+    # the workspace size depends on B*H and N only: with N_pad = 256 > ceil(N/64)*64 the refusal
+    # names the same size as workspace_bytes(B*H, N). (No call here passes every check: on a host
+    # with a GPU such a call would launch kernels on these made-up addresses.)
     need = L.workspace_bytes(1, 64)
     assert need == L.workspace_bytes(1, 33)
     rc = L.lib.sage_kv_prologue(0, 1, 1, 0, 1, p16, 64 * 128, 64 * 128, 128, p16, 64 * 128,
                                 64 * 128, 128, 1, 1, 64, 256, 128, p16, p16, p16, p16, None,
-                                None, p16, None, ctypes.c_void_p(256), need, None)
-    assert b"workspace" not in L.lib.sage_last_error()
-    rc = L.lib.sage_kv_prologue(0, 1, 1, 0, 1, p16, 64 * 128, 64 * 128, 128, p16, 64 * 128,
-                                64 * 128, 128, 1, 1, 64, 256, 128, p16, p16, p16, p16, None,
                                 None, p16, None, ctypes.c_void_p(256), need - 8, None)
     assert rc == 1 and b"workspace" in L.lib.sage_last_error()
+    assert b"need %d bytes" % need in L.lib.sage_last_error()
     # the no-allocation prologue refuses, before touching a GPU, a call whose workspace exceeds
     # its static scratch (4 MiB): here 4096 planes need 8 MiB
     assert L.workspace_bytes(4096, 64) > (4 << 20) >= L.workspace_bytes(24, 9000)
@@ -150,13 +148,29 @@ def test_library_host_calls_without_a_gpu():
     assert b"iters" in L.lib.sage_last_error()
     assert L.lib.sage_mfma_peak_probe(0, 8, 8, ctypes.c_void_p(12), None) == 1
     assert b"aligned" in L.lib.sage_last_error()
-    # B*H beyond 65535 is a valid shape (the grids are 1-D); only the int32 block index bounds it
-    rc = L.lib.sage_attn_fwd(0, 1, 0, p16, 8, 8, 8, None, None, None, None, p16, 8, 8, 8,
-                             1, 70000, 100, 128, ctypes.c_float(0.1), None)
-    assert b"grid" not in L.lib.sage_last_error()
+    # B*H beyond 65535 is a valid shape (the grids are 1-D); HIP's 2^32-1 threads per launch bound
+    # each grid: 128-query blocks of 256 threads and 256-query blocks of 512 (main loop), 64-row
+    # blocks of 64 threads (Q quantizer), one 256-thread block per plane at B*H >= 2048 (prologue)
+    def fwd(H, N):
+        return L.lib.sage_attn_fwd(0, 1, 0, p16, 8, 8, 8, None, None, None, None, p16, 8, 8, 8,
+                                   1, H, N, (N + 63) // 64 * 64, ctypes.c_float(0.1), None)
+    assert fwd(70000, 100) == 1 and b"NULL" in L.lib.sage_last_error()
+    assert fwd((1 << 17) - 1, 16384) == 1 and b"NULL" in L.lib.sage_last_error()
+    assert fwd(1 << 17, 16384) == 1 and b"grid" in L.lib.sage_last_error()
+    assert fwd((1 << 17) - 1, 16385) == 1 and b"grid" in L.lib.sage_last_error()
     rc = L.lib.sage_attn_fwd(0, 1, 0, p16, 8, 8, 8, None, None, None, None, p16, 8, 8, 8,
                              1 << 20, 1 << 12, 1 << 10, 1 << 10, ctypes.c_float(0.1), None)
     assert rc == 1 and b"grid" in L.lib.sage_last_error()
+    def qq(H, N):
+        return L.lib.sage_quant_q(0, 1, p16, 8, 8, 8, 1, H, N, 128, ctypes.c_float(0.1), None,
+                                  None, None, None)
+    assert qq((1 << 20) - 1, 2048) == 1 and b"NULL" in L.lib.sage_last_error()
+    assert qq(1 << 20, 2048) == 1 and b"grid" in L.lib.sage_last_error()
+    def pro(H):
+        return L.lib.sage_kv_prologue(0, 1, 1, 0, 1, p16, 8, 8, 8, p16, 8, 8, 8, 1, H, 64, 64,
+                                      128, *([None] * 9), 0, None)
+    assert pro((1 << 24) - 1) == 1 and b"NULL" in L.lib.sage_last_error()
+    assert pro(1 << 24) == 1 and b"grid" in L.lib.sage_last_error()
     # the main loop on SK / SV' and the mean alone refuse like the others
     def sk(**kw):
         a = dict(dtype=0, qk_int8=1, causal=0, D=128, H_kv=1, N_kv=100, sk=p16)
