@@ -117,3 +117,33 @@ def emulate_rows(q, k, v, rows, *, tensor_layout="HND", is_causal=False, smooth_
                                vmean=None if vmean is None else vmean[kvp])
     lse = oracle.row_lse(lse2, qr, None if mean is None else mean[kvp], sm)
     return o.view(B, H, len(rows), D), lse.view(B, H, len(rows))
+
+
+def quantized_bit_exact(k, v, layout, k_int8):
+    """The prologue's mu, K8, SK, V8T, SV' and S through the C ABI (cuda:0) against the oracle's:
+    True when every byte matches. The outputs are prefilled with sentinels, so unwritten pad rows
+    fail."""
+    import oracle
+    from sageattention.sk1_backend.sk1_loader import SageLib
+    lib = SageLib.get()
+    kk, vv = (oracle.to_hnd(t, layout) for t in (k, v))
+    B, H, N, D = kk.shape
+    BH, n_pad = B * H, oracle.n_pad_for(N)
+    dev = torch.device("cuda:0")
+    k8 = torch.full((BH, n_pad, D), 0x5A, device=dev, dtype=torch.uint8)
+    k8 = k8.view(torch.int8 if k_int8 else torch.float8_e4m3fn)
+    v8t = torch.full((BH, D, n_pad), 0x5A, device=dev, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    sk, sv = (torch.full((BH, n_pad), float("nan"), device=dev) for _ in range(2))
+    s = torch.full((BH,), float("nan"), device=dev)
+    mean = torch.full((BH, D), float("nan"), device=dev)
+    ws = torch.empty(lib.workspace_bytes(BH, N), device=dev, dtype=torch.uint8)
+    lib.kv_prologue(kk.cuda(), vv.cuda(), k8, sk, v8t, sv, s, mean, ws, k_int8=k_int8,
+                    smooth_k=True, fold=True, n_pad=n_pad)
+    torch.cuda.synchronize()
+    kr, vr = kk.reshape(BH, N, D), vv.reshape(BH, N, D)
+    mu = oracle.kseq_mean(kr)
+    r_k8, r_sk = oracle.quant_k(kr, n_pad, mean=mu, int8=k_int8)
+    r_v8t, r_sv = oracle.quant_v(vr, n_pad)
+    r_s, r_svp = oracle.fold_v_scale(r_sv)
+    pairs = ((mean, mu), (k8, r_k8), (sk, r_sk), (v8t, r_v8t), (sv, r_svp), (s, r_s))
+    return all(bytes_equal(g.cpu(), r) for g, r in pairs)

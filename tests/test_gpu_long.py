@@ -12,8 +12,7 @@ import pytest
 import torch
 
 import oracle
-from parity_report import quantized_bit_exact
-from sage_testutil import cosine, have_gfx950, make_qkv, rel_l1
+from sage_testutil import cosine, have_gfx950, make_qkv, quantized_bit_exact, rel_l1
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not have_gfx950(), reason="needs a gfx950 GPU")]
