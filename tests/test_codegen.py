@@ -6,8 +6,10 @@ drops the inactive lanes' operand rows. The compiler is free to sink an MFMA who
 used inside a divergent branch (the epilogue's `qrow < N` store) into that branch, which once
 broke every ragged non-causal call; the kernel source prevents it, and this test keeps it so.
 """
+import functools
 import os
 import re
+import shutil
 import subprocess
 import sys
 
@@ -18,6 +20,7 @@ PKG = os.path.join(ROOT, "sageattention-rdna4_amd")
 sys.path.insert(0, PKG)
 
 
+@functools.lru_cache(maxsize=None)
 def _assembly(source):
     import build_lib
     if not os.path.exists(build_lib.HIPCC):
@@ -339,3 +342,266 @@ def test_resource_parser_sees_a_spill():
     meta = ("  - .agpr_count:     0\n    .name:           _Zk\n    .private_segment_fixed_size: 12\n"
             "    .vgpr_count:     168\n    .vgpr_spill_count: 3\n.end_amdgpu_metadata\n")
     assert _kernel_resources(meta) == [("_Zk", 168, 3, 12)]
+
+
+# ---------------------------------------------------------------------------------------------
+# Barrier liveness. A workgroup whose waves execute different numbers of `s_barrier` hangs the
+# GPU. In the ping-pong kernel each wave computes up to its own causal diagonal (w_end differs by
+# wave) and then only stages, keeping 2 barriers per 64-key block, so the totals agree only by
+# construction. `asm_sim` interprets each kernel's assembly per wave for concrete arguments
+# (scalar control flow exactly; data-dependent branches both ways, which must agree on their
+# barrier count) and counts the barriers each wave executes; every wave must execute the same
+# number, on shapes that cover causal and non-causal grids, ragged tails, grouped K/V heads, a
+# key length of its own and the optional outputs.
+# ---------------------------------------------------------------------------------------------
+import asm_sim  # noqa: E402
+
+_FAKE = 0x20000000                     # device addresses the interpreter never dereferences
+
+
+def _fake(i):
+    return _FAKE + (i << 24)
+
+
+def _cdiv(a, b):
+    return (a + b - 1) // b
+
+
+def _template(name):
+    """(bf16, qk_int8, causal, head_dim or None) of a main-loop kernel's mangled name."""
+    m = re.search(r"I(DF16_|DF16b)Lb([01])ELb([01])E(?:Li(\d+)E)?", name)
+    return m.group(1) == "DF16b", m.group(2) == "1", m.group(3) == "1", \
+        int(m.group(4)) if m.group(4) else 128
+
+
+def _attn_args(family, N, Nk, H, H_kv, D, lse=False, vmean=False):
+    """Kernel arguments in signature order, as the launchers in attn_fwd*.hip form them (B = 1,
+    contiguous HND), and the number of workgroups."""
+    bm = 256 if family == "pp" else 128
+    num_qt = _cdiv(N, bm)
+    total = num_qt * H
+    strides = [H * N * D, N * D, D] * 2
+    tail = [H, H_kv, H // H_kv, N, Nk, _cdiv(Nk, 64) * 64, num_qt, total // 8 * 8, 0.088,
+            _fake(9) if lse else 0, _fake(10) if lse else 0, _fake(11) if vmean else 0]
+    if family == "pl":
+        plane = 2 * _cdiv(Nk, 64) * 64
+        head = [_fake(0), _fake(1), _fake(2), plane, 128, _fake(2) + 256, plane, 128, 1.0,
+                _fake(3), _fake(4), _fake(5)]
+    else:
+        head = [_fake(0), _fake(1), _fake(2), _fake(3), _fake(4), _fake(5)]
+    return head + strides + tail, total
+
+
+# (N, N_kv, H, H_kv, lse, vmean): causal calls use N == N_kv
+_CAUSAL_SHAPES = [(1, 1, 1, 1, False, False), (200, 200, 2, 1, True, False),
+                  (777, 777, 1, 1, False, True)]
+_NONCAUSAL_SHAPES = [(1, 1, 1, 1, False, False), (300, 777, 4, 2, True, True),
+                     (777, 65, 1, 1, False, False), (513, 512, 1, 1, False, False)]
+
+
+def _pick(total):
+    ids = sorted({0, 1, total // 2, total - 2, total - 1} & set(range(total)))
+    return ids
+
+
+def _main_loop_cases(asm):
+    for name in asm_sim.kernel_functions(asm):
+        fam = ("pp" if "attn_fwd_pp_kernel" in name else "pl" if "attn_fwd_pl_kernel" in name
+               else "q" if "attn_fwd_kernel" in name else None)
+        if fam is None:
+            continue
+        _, _, causal, D = _template(name)
+        for N, Nk, H, H_kv, lse, vm in (_CAUSAL_SHAPES if causal else _NONCAUSAL_SHAPES):
+            vals, total = _attn_args(fam, N, Nk, H, H_kv, D, lse, vm)
+            for wg in _pick(total):
+                yield name, vals, wg, (N, Nk, H, H_kv, wg)
+
+
+@pytest.mark.parametrize("source", ["attn_fwd.hip", "attn_fwd_pp.hip", "attn_fwd_pl.hip"])
+def test_every_wave_of_a_main_loop_block_executes_the_same_barriers(source):
+    asm = _assembly(os.path.join(PKG, "csrc", source))
+    seen = 0
+    for name, vals, wg, case in _main_loop_cases(asm):
+        counts, _ = asm_sim.barrier_counts(asm, name, vals, wg)
+        assert len(set(counts)) == 1 and counts[0] > 0, (name, case, counts)
+        seen += 1
+    assert seen >= 20
+
+
+def _prologue_geom(BH, N, N_pad, step):
+    # prologue_geom (prologue.hip): one round of resident blocks on 256 CUs, 3 stats blocks and
+    # 8 quant blocks per CU
+    per = lambda slots: slots // BH if BH < slots else 1  # noqa: E731
+    nc = _cdiv(N, 64) * 64
+    r1 = _cdiv(_cdiv(nc, per(256 * 3)), step) * step
+    r2 = _cdiv(_cdiv(N_pad, per(256 * 8)), 64) * 64
+    return r1, _cdiv(nc, r1), r2, _cdiv(N_pad, r2)
+
+
+def test_every_wave_of_a_prologue_block_executes_the_same_barriers():
+    asm = _assembly(os.path.join(PKG, "csrc", "prologue.hip"))
+    seen = 0
+    for name in asm_sim.kernel_functions(asm):
+        m = re.search(r"(kv_stats_kernel|k_quant_kernel)I(DF16_|DF16b)L(b|i)([0-9])ELi(\d+)E",
+                      name)
+        if not m:
+            continue
+        D = int(m.group(5))
+        step = 8 * (256 // (D // 8))
+        for BH, N, extra_pad in ((2, 777, 0), (1, 5000, 128), (800, 64, 0)):
+            n_pad = _cdiv(N, 64) * 64 + extra_pad
+            r1, c1, r2, c2 = _prologue_geom(BH, N, n_pad, step)
+            st = [BH * N * D, N * D, D]
+            if m.group(1) == "kv_stats_kernel":
+                vals = [_fake(0), _fake(1), _fake(2), _fake(3), _fake(4), _fake(5), _fake(6),
+                        _fake(7), BH, N, n_pad, r1, c1] + st + st + [1]
+                total = c1 * BH
+            else:
+                vals = [_fake(0), _fake(1), _fake(2), _fake(3), _fake(4), _fake(5), _fake(6),
+                        _fake(7), _fake(8), BH, N, n_pad, r2, c2, c1] + st + [1, 1]
+                total = c2 * BH
+            for wg in _pick(total):
+                counts, _ = asm_sim.barrier_counts(asm, name, vals, wg)
+                assert len(set(counts)) == 1 and counts[0] > 0, (name, BH, N, wg, counts)
+                seen += 1
+    assert seen >= 50
+
+
+def _mutated_assembly(tmp_path, source, old, new, compile_source=None):
+    """hipcc -S of `compile_source` (default `source`) in a copy of csrc/ in which `old` is
+    replaced by `new` in `source`."""
+    import build_lib
+    src = tmp_path / "csrc"
+    shutil.copytree(os.path.join(PKG, "csrc"), src)
+    inc = tmp_path / "include"
+    shutil.copytree(os.path.join(ROOT, "include"), inc)
+    path = src / source
+    text = path.read_text()
+    assert old in text
+    path.write_text(text.replace(old, new))
+    target = compile_source or source
+    flags = [f for f in build_lib.COMMON_FLAGS if f not in ("-fPIC",)]
+    flags += build_lib.FILE_FLAGS.get(target, [])
+    res = subprocess.run([build_lib.HIPCC] + flags + ["--cuda-device-only", "-S", "-o", "-",
+                                                      str(src / target)],
+                         capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-2000:]
+    return res.stdout
+
+
+def _pp_causal_int8(asm):
+    return next(n for n in asm_sim.kernel_functions(asm)
+                if "attn_fwd_pp_kernel" in n and _template(n)[1:3] == (True, True))
+
+
+def test_barrier_check_flags_a_staging_tail_that_starts_one_block_late(tmp_path):
+    # Planted in a copy of the ping-pong: the staging-only blocks after a wave's diagonal start
+    # one block late, so the waves whose diagonal ends early execute two barriers fewer.
+    asm = _mutated_assembly(tmp_path, "attn_fwd_pp.hip", "for (j = w_end; j < j_end; ++j) {",
+                            "for (j = w_end + 1; j < j_end; ++j) {")
+    name = _pp_causal_int8(asm)
+    # the last q-tile (rows 768..1023, run first): the waves' diagonals end at blocks 13 .. 16
+    vals, total = _attn_args("pp", 1024, 1024, 1, 1, 128)
+    counts, _ = asm_sim.barrier_counts(asm, name, vals, 0)
+    assert len(set(counts)) > 1, counts
+    good = _assembly(os.path.join(PKG, "csrc", "attn_fwd_pp.hip"))
+    counts, _ = asm_sim.barrier_counts(good, _pp_causal_int8(good), vals, 0)
+    assert len(set(counts)) == 1, counts
+
+
+def test_barrier_check_flags_a_barrier_under_a_data_dependent_branch(tmp_path):
+    # Planted: a barrier inside the accumulator rescale, which a wave runs only when some lane's
+    # running maximum moved -- a data-dependent count.
+    asm = _mutated_assembly(tmp_path, "attn_common.h",
+                            "  if (__any(alpha != 1.0f)) {\n",
+                            "  if (__any(alpha != 1.0f)) {\n    __syncthreads();\n",
+                            compile_source="attn_fwd_pp.hip")
+    with pytest.raises(asm_sim.DataDependentBarrier):
+        for name, vals, wg, _ in _main_loop_cases(asm):
+            asm_sim.barrier_counts(asm, name, vals, wg)
+
+
+def test_interpreter_follows_scalar_control_flow():
+    # a counted loop whose trip count comes from a kernel argument, a wave-dependent branch and a
+    # data-dependent one (a global load) around barrier-free code
+    asm = """_Zk:
+ s_load_dword s4, s[0:1], 0x0
+ v_lshrrev_b32_e32 v1, 6, v0
+ v_readfirstlane_b32 s5, v1
+ s_waitcnt lgkmcnt(0)
+.LBB0_1:
+ s_barrier
+ s_add_i32 s4, s4, -1
+ s_cmp_lg_u32 s4, 0
+ s_cbranch_scc1 .LBB0_1
+ s_cmp_eq_u32 s5, 1
+ s_cbranch_scc1 .LBB0_3
+ global_load_dword v2, v1, s[0:1]
+ s_waitcnt vmcnt(0)
+ v_cmp_eq_u32_e32 vcc, 0, v2
+ s_cbranch_vccnz .LBB0_3
+ v_add_u32_e32 v3, v2, v2
+.LBB0_3:
+ s_barrier
+ s_endpgm
+.Lfunc_end0:
+"""
+    meta = """
+  - .agpr_count:     0
+    .args:
+      - .offset:         0
+        .size:           4
+        .value_kind:     by_value
+    .max_flat_workgroup_size: 128
+    .name:           _Zk
+.amdhsa_kernel _Zk
+    .amdhsa_user_sgpr_count 2
+    .amdhsa_user_sgpr_kernarg_segment_ptr 1
+    .amdhsa_system_sgpr_workgroup_id_x 1
+.end_amdhsa_kernel
+"""
+    counts, _ = asm_sim.barrier_counts(asm + meta, "_Zk", [5], 0)
+    assert counts == [6, 6]
+    bad = asm.replace(" v_add_u32_e32 v3, v2, v2\n", " s_barrier\n")
+    with pytest.raises(asm_sim.DataDependentBarrier):
+        asm_sim.barrier_counts(bad + meta, "_Zk", [5], 0)
+    skewed = asm.replace(".LBB0_3:\n s_barrier\n", ".LBB0_3:\n")\
+        .replace(" s_cbranch_scc1 .LBB0_3\n global_load", " s_cbranch_scc1 .LBB0_4\n global_load")\
+        .replace(" s_endpgm\n", " s_endpgm\n.LBB0_4:\n s_barrier\n s_endpgm\n")
+    counts, _ = asm_sim.barrier_counts(skewed + meta, "_Zk", [5], 0)
+    assert counts == [5, 6]
+
+
+# ---------------------------------------------------------------------------------------------
+# The hot loop's instruction budget (the reference's method: count instructions per matrix
+# instruction in the hot loop against a budget). The interpreter counts the vector ALU
+# instructions each wave executes, along the cheaper side of every data-dependent branch (the
+# accumulator rescale runs only when a row maximum moves), so the difference between two key
+# lengths is the per-block cost of the steady state. Per 64-key block of one wave (32 queries):
+# 12 MFMAs with int8 Q.K (8 for S^T, 4 for P.V), 8 with e4m3 Q.K; the VALU count is held to the
+# committed budget, so a change that should cut it and does not is caught before it is timed.
+# ---------------------------------------------------------------------------------------------
+PP_VALU_BUDGET = {True: 244, False: 212}     # qk_int8 -> VALU per wave and 64-key block
+
+
+def pp_block_costs(asm, name):
+    """Per-wave (VALU, MFMA) per 64-key block of the ping-pong in its steady state (one q-tile,
+    non-causal, 8 more key blocks)."""
+    res = []
+    for nk in (640, 1152):
+        vals, _ = _attn_args("pp", 256, nk, 1, 1, 128)
+        _, states = asm_sim.barrier_counts(asm, name, vals, 0)
+        res.append([(s.valu, s.mfma) for s in states])
+    return [((b[0] - a[0]) / 8.0, (b[1] - a[1]) / 8.0) for a, b in zip(*res)]
+
+
+@pytest.mark.parametrize("qk_int8", [True, False])
+def test_ping_pong_instruction_budget(qk_int8):
+    asm = _assembly(os.path.join(PKG, "csrc", "attn_fwd_pp.hip"))
+    name = next(n for n in asm_sim.kernel_functions(asm)
+                if "attn_fwd_pp_kernel" in n and _template(n)[1:3] == (qk_int8, False)
+                and not _template(n)[0])
+    costs = pp_block_costs(asm, name)
+    assert all(m == (12 if qk_int8 else 8) for _, m in costs), costs
+    worst = max(v for v, _ in costs)
+    assert worst <= PP_VALU_BUDGET[qk_int8], (worst, costs)
