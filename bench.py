@@ -31,7 +31,9 @@ Prints ONE JSON line. Besides the contract fields it carries
   FETCH_SIZE/WRITE_SIZE summary for the workload (null when none is committed);
 * `prologue`: the prologue pair's achieved HBM GB/s on its algorithmic bytes;
 * `cpu_baseline`: the CPU emulation of the reference scheme (`oracle/`, a "port") and torch CPU
-  SDPA, timed on a bounded sample of the same workload on this host's cores.
+  SDPA, timed on a bounded sample of the same workload on this host's cores;
+* `first_call`: a fresh child process's import, library load and first call of the workload's
+  shape (the reference quotes its first call in a fresh process, `README.md:77-79`).
 """
 import argparse
 import json
@@ -331,6 +333,57 @@ def copy_calibration(mib, reps):
     return 0
 
 
+def first_call_child(workload):
+    """Run in a fresh child process: time the import of torch, the import of the package, the
+    library load, and the first and second `sageattn` calls of `workload`'s shape (inputs made on
+    the GPU, outside the timed calls). Prints one JSON line."""
+    t0 = time.perf_counter()
+    import torch
+    t1 = time.perf_counter()
+    from sageattention import sageattn
+    from sageattention.sk1_backend import SageLib
+    t2 = time.perf_counter()
+    SageLib.get()
+    t3 = time.perf_counter()
+    dt, B, H, N, causal, layout, *_ = WORKLOADS[workload]
+    D = head_dim(WORKLOADS[workload])
+    shape = (B, H, N, D) if layout == "HND" else (B, N, H, D)
+    dtype = torch.float16 if dt == "fp16" else torch.bfloat16
+    q, k, v = (torch.randn(shape, device="cuda:0", dtype=dtype) for _ in range(3))
+    torch.cuda.synchronize()
+    t4 = time.perf_counter()
+    sageattn(q, k, v, tensor_layout=layout, is_causal=causal, smooth_k=True)
+    torch.cuda.synchronize()
+    t5 = time.perf_counter()
+    sageattn(q, k, v, tensor_layout=layout, is_causal=causal, smooth_k=True)
+    torch.cuda.synchronize()
+    t6 = time.perf_counter()
+    print(json.dumps({"import_torch_s": round(t1 - t0, 4), "import_package_s": round(t2 - t1, 4),
+                      "library_load_s": round(t3 - t2, 4), "first_call_s": round(t5 - t4, 4),
+                      "second_call_s": round(t6 - t5, 4),
+                      "import_to_first_result_s": round((t1 - t0) + (t3 - t1) + (t5 - t4), 4)}),
+          flush=True)
+    return 0
+
+
+def first_call_latency(workload, timeout_s=600):
+    """`first_call_child` in a fresh process (started before this process touches the GPU), or
+    the reason it could not be measured."""
+    import subprocess
+    try:
+        res = subprocess.run([sys.executable, os.path.abspath(__file__), "--first-call-child",
+                              "--workload", workload], capture_output=True, text=True,
+                             timeout=timeout_s)
+    except subprocess.TimeoutExpired:
+        return {"error": "timed out after %d s" % timeout_s}
+    lines = [ln for ln in res.stdout.splitlines() if ln.startswith("{")]
+    if res.returncode != 0 or not lines:
+        return {"error": "child exited %d: %s" % (res.returncode, res.stderr.strip()[-300:])}
+    out = json.loads(lines[-1])
+    out["process"] = "fresh child process, the workload's shape; inputs made on the GPU"
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -351,6 +404,10 @@ def main():
     ap.add_argument("--kernel", type=int, default=0, choices=(0, 1, 2, 3),
                     help="main-loop kernel: 0 the library's choice by grid fill, 1 the 128-query "
                          "kernel, 2 the 256-query ping-pong, 3 the pipelined 128-query kernel")
+    ap.add_argument("--no-first-call", action="store_true",
+                    help="skip the fresh-process first-call latency (import, library load, first "
+                         "call)")
+    ap.add_argument("--first-call-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of the benchmark, run a plain device copy of this many MiB "
                          "(the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -359,6 +416,12 @@ def main():
         print("bench.py: this build measures one GPU only (every GPU box here has one GPU); "
               "--gpus %d is not supported" % args.gpus, file=sys.stderr)
         return 2
+    if args.first_call_child:
+        return first_call_child(args.workload)
+    # before this process initializes the GPU: the first call in a fresh process
+    first = None if args.no_first_call or args.copy_mib else first_call_latency(args.workload)
+    if first is not None:
+        log("first call:", first)
 
     import torch
     if args.copy_mib:
@@ -489,6 +552,7 @@ def main():
         "prologue": {"ms": round(pro_ms, 4), "bytes": pbytes, "achieved_GBps": round(pro_gbps, 1),
                      "peak_GBps": HBM_PEAK_GBPS, "frac": round(pro_gbps / HBM_PEAK_GBPS, 4)},
         "cpu_baseline": cpu,
+        "first_call": first,
         # the timed region's HIP-event time per call, the split pass's per-call times, and the
         # shader clock before and after the timed region: box-to-box clock differences are the
         # largest source of spread between runs

@@ -170,3 +170,13 @@ def test_board_power_reads_hwmon(bench, tmp_path):
     (h1 / "power1_average").write_text("1200000000\n")
     assert bench.board_power(str(tmp_path))["watts"] == 1200.0
     assert bench.board_power(str(tmp_path / "nothing")) is None
+
+
+def test_first_call_latency_reports_a_child_failure(bench):
+    # The first-call figure comes from a fresh child process; where it cannot run (no GPU here)
+    # the field carries the reason instead of a number, and the parent goes on.
+    out = bench.first_call_latency("c1", timeout_s=300)
+    if "error" in out:
+        assert "child exited" in out["error"] or "timed out" in out["error"]
+    else:
+        assert out["first_call_s"] > 0 and out["library_load_s"] >= 0
