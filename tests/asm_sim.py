@@ -217,19 +217,24 @@ class State:
     """SGPRs: index -> 32-bit int (absent = UNKNOWN). VGPRs: index -> (values uint32[64],
     known bool[64]). SCC: 0, 1 or None. `valu`, `mfma`: vector ALU instructions other than MFMAs,
     and MFMAs, executed so far (along the cheaper side of every data-dependent branch)."""
-    __slots__ = ("s", "v", "scc", "barriers", "valu", "mfma", "ebound")
+    __slots__ = ("s", "v", "scc", "barriers", "valu", "mfma", "ebound", "marks")
 
     def __init__(self):
         self.s, self.v, self.scc, self.barriers, self.valu, self.mfma = {}, {}, None, 0, 0, 0
         self.ebound = FULL      # a known superset of EXEC (EXEC itself may be UNKNOWN)
+        self.marks = []         # (valu, mfma) at each barrier
 
     def copy(self):
         c = State()
         c.s = dict(self.s)
         c.v = {k: (a.copy(), k_.copy()) for k, (a, k_) in self.v.items()}
         c.scc, c.barriers, c.valu, c.mfma = self.scc, self.barriers, self.valu, self.mfma
-        c.ebound = self.ebound
+        c.ebound, c.marks = self.ebound, list(self.marks)
         return c
+
+    def phases(self):
+        """(VALU, MFMA) executed between consecutive barriers."""
+        return [(b[0] - a[0], b[1] - a[1]) for a, b in zip(self.marks, self.marks[1:])]
 
 
 def merge(a, b):
@@ -246,6 +251,7 @@ def merge(a, b):
     m.barriers = a.barriers
     m.valu, m.mfma = min(a.valu, b.valu), min(a.mfma, b.mfma)
     m.ebound = a.ebound | b.ebound
+    m.marks = list(a.marks)
     return m
 
 
@@ -423,6 +429,7 @@ class Machine:
                 raise Unsupported(I.text)
             if mn == "s_barrier":
                 st.barriers += 1
+                st.marks.append((st.valu, st.mfma))
                 continue
             if mn.startswith("s_"):
                 self.salu(st, I)

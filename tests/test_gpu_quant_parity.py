@@ -276,3 +276,57 @@ def test_prologue_grid_regimes(dtype, k_int8, B, H, N):
     assert bytes_equal(got["mean"], ref["mean"]), mismatch_report(got["mean"], ref["mean"], "mean")
     for name, rname in (("k8", "k8"), ("sk", "sk"), ("v8t", "v8t"), ("sv", "svp"), ("s", "s")):
         assert bytes_equal(got[name], ref[rname]), mismatch_report(got[name], ref[rname], name)
+
+
+@pytest.mark.parametrize("extra", [256, 1024])
+@pytest.mark.parametrize("dtype,k_int8", [(torch.float16, True), (torch.bfloat16, False)])
+def test_prologue_with_padding_beyond_the_last_block(dtype, k_int8, extra):
+    # N_pad may exceed ceil(N/64)*64 (the contract asks only for a multiple of 64 >= N): the
+    # stats pass's last block then covers every pad row. K8, SK, V8T, SV', S and the mean must
+    # equal the oracle's tensors padded to that length (pad rows: K8 0, SK 1.0, V8T 0, SV' 0),
+    # KCONST must hold SK and RN(SV'*448) of every block, and the main loop on these tensors must
+    # give the bits of the same call with the normal padding (the extra keys are masked: p = 0).
+    lib = _lib()
+    N, H = 300, 2
+    q, k, v = make_qkv(1, H, N, seed=71, dtype=dtype, k_offset_std=2.0, outlier_frac=0.01)
+    print("case", dtype, k_int8, extra, flush=True)
+    dev = torch.device("cuda:0")
+    kd, vd, qd = k.to(dev), v.to(dev), q.to(dev)
+    outs = {}
+    for n_pad in (oracle.n_pad_for(N), oracle.n_pad_for(N) + extra):
+        BH, D = H, HEAD_DIM
+        k8 = torch.full((BH, n_pad, D), 0x5A, device=dev, dtype=torch.uint8)
+        k8 = k8.view(torch.int8 if k_int8 else torch.float8_e4m3fn)
+        v8t = torch.full((BH, D, n_pad), 0x5A, device=dev, dtype=torch.uint8).view(
+            torch.float8_e4m3fn)
+        sk, sv = (torch.full((BH, n_pad), float("nan"), device=dev) for _ in range(2))
+        s = torch.full((BH,), float("nan"), device=dev)
+        mean = torch.full((BH, D), float("nan"), device=dev)
+        kc = torch.full((BH, n_pad // 64, 2, 64), float("nan"), device=dev)
+        ws = torch.full((lib.workspace_bytes(BH, N),), 0xFF, device=dev, dtype=torch.uint8)
+        lib.kv_prologue(kd, vd, k8, sk, v8t, sv, s, mean, ws, k_int8=k_int8, smooth_k=True,
+                        fold=True, n_pad=n_pad, kconst=kc)
+        o = torch.full_like(qd, float("nan"))
+        for kernel in (2, 3):
+            o.fill_(float("nan"))
+            lib.attn_fwd(qd, k8, kc, v8t, s, o, qk_int8=k_int8, causal=False, sm_scale=D ** -0.5,
+                         n_pad=n_pad, kernel=kernel)
+            torch.cuda.synchronize()
+            outs[(n_pad, kernel)] = o.cpu()
+        kr, vr = k.reshape(BH, N, D), v.reshape(BH, N, D)
+        mu = oracle.kseq_mean(kr)
+        r_k8, r_sk = oracle.quant_k(kr, n_pad, mean=mu, int8=k_int8)
+        r_v8t, r_sv = oracle.quant_v(vr, n_pad)
+        r_s, r_svp = oracle.fold_v_scale(r_sv)
+        for got, ref, name in ((mean, mu, "mean"), (k8, r_k8, "k8"), (sk, r_sk, "sk"),
+                               (v8t, r_v8t, "v8t"), (sv, r_svp, "svp"), (s, r_s, "s")):
+            g = got.cpu()
+            assert bytes_equal(g, ref), mismatch_report(g, ref, name)
+        kcc = kc.cpu()
+        assert bytes_equal(kcc[:, :, 0, :].reshape(BH, n_pad), r_sk)
+        assert bytes_equal(kcc[:, :, 1, :].reshape(BH, n_pad), (r_svp * 448.0).float())
+    base = oracle.n_pad_for(N)
+    for kernel in (2, 3):
+        a, b = outs[(base, kernel)], outs[(base + extra, kernel)]
+        assert torch.isfinite(b.float()).all()
+        assert bytes_equal(a, b), (kernel, mismatch_report(a, b, "o"))
