@@ -401,9 +401,10 @@ def main():
     ap.add_argument("--workload", default="c3c", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
-    ap.add_argument("--kernel", type=int, default=0, choices=(0, 1, 2, 3),
+    ap.add_argument("--kernel", type=int, default=0, choices=(0, 1, 2, 3, 4),
                     help="main-loop kernel: 0 the library's choice by grid fill, 1 the 128-query "
-                         "kernel, 2 the 256-query ping-pong, 3 the pipelined 128-query kernel")
+                         "kernel, 2 the 256-query ping-pong, 3 the pipelined 128-query kernel, "
+                         "4 its key split (non-causal head_dim 64)")
     ap.add_argument("--no-first-call", action="store_true",
                     help="skip the fresh-process first-call latency (import, library load, first "
                          "call)")
@@ -447,7 +448,8 @@ def main():
         timed_call = "sk1_forward(kernel=%d)" % args.kernel
     # the kernel the timed call runs: the library's own automatic choice for kernel 0
     kcode = args.kernel or lib.kernel_choice(B, H, N, D, causal)
-    kname = {1: "attn_fwd_kernel", 2: "attn_fwd_pp_kernel", 3: "attn_fwd_pl_kernel"}[kcode]
+    kname = {1: "attn_fwd_kernel", 2: "attn_fwd_pp_kernel", 3: "attn_fwd_pl_kernel",
+             4: "attn_fwd_pl_kernel (key split)"}[kcode]
     sync = torch.cuda.synchronize
     event = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     for _ in range(args.warmup):

@@ -35,11 +35,15 @@ extern "C" {
 #define SAGE_F16 0
 #define SAGE_BF16 1
 
-/* main-loop kernel choice of sage_attn_fwd_ex (all give the same bits) */
+/* main-loop kernel choice of sage_attn_fwd_ex (the first three give the same bits) */
 #define SAGE_KERNEL_AUTO 0  /* by grid fill on this device: sage_attn_kernel_choice */
 #define SAGE_KERNEL_Q128 1  /* 128 queries per block of 4 waves */
 #define SAGE_KERNEL_Q256 2  /* 256 queries per block of 8 waves, two groups in ping-pong */
 #define SAGE_KERNEL_PIPE 3  /* 128 queries per block of 4 waves, MFMAs pipelined inside each wave */
+#define SAGE_KERNEL_SPLIT 4 /* SAGE_KERNEL_PIPE with the key blocks split between two wave pairs
+                               and merged in-block: 64 queries per block; non-causal head_dim 64
+                               only (grids that would leave compute units idle); the same P, sums
+                               in another order: rounding-level different output bits */
 
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH: 200 (0.2.0). 0.2.0 changed KCONST from
  * three rows per 64-key block to the two above; a caller built against 0.1.0 (100) that allocates
@@ -158,12 +162,17 @@ int sage_attn_fwd(int dtype, int qk_int8, int causal,
 /*
  * sage_attn_fwd generalized: grouped K/V heads, a key length of its own, the main-loop kernel
  * chosen by the caller (SAGE_KERNEL_*) and an optional per-row logsumexp. sage_attn_fwd is this
- * with H_kv = H, N_kv = N, SAGE_KERNEL_AUTO and no logsumexp. Both kernels compute the same
- * arithmetic in the same order per query; only the block shape and schedule differ. The kernel
- * choice has no counterpart in the reference (one kernel per dtype there).
+ * with H_kv = H, N_kv = N, SAGE_KERNEL_AUTO and no logsumexp. SAGE_KERNEL_Q128, _Q256 and _PIPE
+ * compute the same arithmetic in the same order per query; only the block shape and schedule
+ * differ. SAGE_KERNEL_SPLIT runs each query's even and odd 64-key blocks on two waves that
+ * exchange their block maxima every block, so each block's probabilities use the sequential
+ * running max (the same P as the other kernels), and merges the two row sums and accumulators at
+ * the end (each scaled by exp2(mc_i - max(mc0, mc1))): only the fp32 sums round differently. The
+ * kernel choice has no counterpart in the reference (one kernel per dtype there).
  *
  *   q, o      logical (B, H, N, D) views, as in sage_attn_fwd
- *   D         head_dim, 64 or 128 (at 64, SAGE_KERNEL_Q256 is refused)
+ *   D         head_dim, 64 or 128 (at 64, SAGE_KERNEL_Q256 is refused; at 128 and with causal,
+ *             SAGE_KERNEL_SPLIT is refused)
  *   k8, kconst, v8t, s   the prologue's outputs for B*H_kv planes of N_kv keys (N_kv_pad =
  *             ceil(N_kv/64)*64). Query head h reads K/V head h / (H / H_kv) (grouped-query and
  *             multi-query attention; H must be a multiple of H_kv), and N may differ from N_kv
@@ -193,11 +202,15 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal,
                      float* lse, const float* kmean, const float* vmean, void* stream);
 
 /*
- * The main-loop kernel SAGE_KERNEL_AUTO runs for a call of this shape: SAGE_KERNEL_Q256 or
- * SAGE_KERNEL_PIPE (all kernels give the same bits; only speed differs). No counterpart in the
- * reference (one kernel per dtype there); for benchmarks and profilers that name the kernel.
+ * The main-loop kernel SAGE_KERNEL_AUTO runs for a call of this shape: SAGE_KERNEL_Q256,
+ * SAGE_KERNEL_PIPE or SAGE_KERNEL_SPLIT (Q128, Q256 and PIPE give the same bits; SPLIT merges two
+ * partial row sums and accumulators and differs from them in the last bits of the output). No
+ * counterpart in the reference (one kernel per dtype there); for benchmarks and profilers that
+ * name the kernel.
  *   cus  compute units to plan for; <= 0: those of the current device (a device query)
- * head_dim 64 runs the pipelined kernel. At 128 the 256-query ping-pong runs when, on `cus` CUs,
+ * head_dim 64 runs the key split when not causal and its grid of 64-query blocks,
+ * B*H*ceil(N/64), is at most 3 per CU (one round: its LDS lets three blocks share a CU), else the
+ * pipelined kernel. At 128 the 256-query ping-pong runs when, on `cus` CUs,
  * its grid is estimated to finish at least 3 % sooner: a causal grid with at least 4 of its
  * blocks per CU, unless padding the last query tile to 256 rows costs over 2 % more of the causal
  * work than padding it to 128; a non-causal one by whole rounds of blocks (up to three 128-query

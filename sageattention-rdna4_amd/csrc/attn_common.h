@@ -276,10 +276,12 @@ __device__ __forceinline__ KeyConsts load_key_consts(const ScaleTile& sc, int la
 struct BlockShift {
   float mc, alpha;
 };
+
+// block_max: the first part of scores_block -- x = fp32(Q8.K8) * SK over the raw scores, masked
+// keys -inf -- returning this lane's query's max over the block's 64 keys.
 template <bool QK_INT8, bool CAUSAL, int NCONV = 0>
-__device__ __forceinline__ BlockShift scores_block(f32x16 (&sx)[2], float sk0, float sk1, int j, int q0,
-                                                   int qrow, int N, int hh, float cq, float& m_x,
-                                                   float& mc) {
+__device__ __forceinline__ float block_max(f32x16 (&sx)[2], float sk0, float sk1, int j, int q0,
+                                           int qrow, int N, int hh) {
   static_for<0, 32>([&](auto ic) {
     constexpr int jj = decltype(ic)::value;
     const float v = sx[jj >> 4][jj & 15];
@@ -299,20 +301,33 @@ __device__ __forceinline__ BlockShift scores_block(f32x16 (&sx)[2], float sk0, f
   float x[32];
 #pragma unroll
   for (int i = 0; i < 32; ++i) x[i] = sx[i >> 4][i & 15];
-  const float mx = max_halves(max32(x));
-  const float m_new = fmaxf(m_x, mx);
-  float mc_new = cq * ((m_new == -INFINITY) ? 0.0f : m_new);
-  // One to two ulps below RN(c_q * m): the max key's exp2 argument c_q*m - mc (exact in the fma)
-  // is then never negative, and probs_block clamps its exp2 to at most 1, so the max key gets
-  // p = 1 exactly, as the reference's exp2(s - m) does. (With the shift RN(c_q*m) the argument
-  // is the product's rounding residual, +-1e-6, and p*W can then round to the other side of an
-  // e4m3 tie: a 6-8% change of the dominant key's weight.) 0 stays 0.
-  mc_new = __builtin_fmaf(__builtin_fabsf(mc_new), -0x1p-23f, mc_new);
-  // mc_new is rounded before it is used: the opaque copy keeps the compiler from fusing the
-  // products into the subtraction below, which it would do or not depending on the surrounding
+  return max_halves(max32(x));
+}
+
+// The exp2 shift of the running max m: c_q * m (0 while m is -inf), lowered by one to two ulps.
+// With that, the max key's exp2 argument c_q*m - mc (exact in the fma) is never negative, and the
+// probabilities' exp2 is clamped to at most 1, so the max key gets p = 1 exactly, as the
+// reference's exp2(s - m) does. (With the shift RN(c_q*m) the argument is the product's rounding
+// residual, +-1e-6, and p*W can then round to the other side of an e4m3 tie: a 6-8% change of the
+// dominant key's weight.) 0 stays 0.
+__device__ __forceinline__ float shift_of(float m, float cq) {
+  float mc = cq * ((m == -INFINITY) ? 0.0f : m);
+  mc = __builtin_fmaf(__builtin_fabsf(mc), -0x1p-23f, mc);
+  // mc is rounded before it is used: the opaque copy keeps the compiler from fusing the products
+  // into the subtraction that forms alpha, which it would do or not depending on the surrounding
   // code (so two kernels would round alpha differently). exp2(mc - mc_new) of the rounded shifts
   // is then exactly 1 for an unmoved max; the select skips the exp2 there.
-  asm volatile("" : "+v"(mc_new));
+  asm volatile("" : "+v"(mc));
+  return mc;
+}
+
+template <bool QK_INT8, bool CAUSAL, int NCONV = 0>
+__device__ __forceinline__ BlockShift scores_block(f32x16 (&sx)[2], float sk0, float sk1, int j, int q0,
+                                                   int qrow, int N, int hh, float cq, float& m_x,
+                                                   float& mc) {
+  const float mx = block_max<QK_INT8, CAUSAL, NCONV>(sx, sk0, sk1, j, q0, qrow, N, hh);
+  const float m_new = fmaxf(m_x, mx);
+  const float mc_new = shift_of(m_new, cq);
   const float alpha = (m_new != m_x) ? __builtin_amdgcn_exp2f(mc - mc_new) : 1.0f;
   m_x = m_new;
   mc = mc_new;

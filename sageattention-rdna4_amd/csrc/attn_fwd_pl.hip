@@ -47,8 +47,10 @@ struct __attribute__((aligned(16))) PlBuf {
   KeyRows c;
 };
 
-// Waves per SIMD the pipelined kernel's register budget is sized for.
-constexpr int pl_waves(int D) { return D == 64 ? 4 : 3; }
+// Waves per SIMD the pipelined kernel's register budget is sized for. The key-split form (head_dim
+// 64) holds two staging rings and the block-max exchange, 52 KB of LDS, so three of its blocks
+// fit a CU.
+constexpr int pl_waves(int D, bool split = false) { return split ? 3 : (D == 64 ? 4 : 3); }
 
 // S^T tile t of a 64-key block (keys 32h + 16t + reg of lane half h) for this lane's query:
 // int8 -- the bits of the int32 Q8.K8; fp8 -- the fp32 dot product.
@@ -106,8 +108,18 @@ __device__ __forceinline__ void probs_tile(const f32x16 (&x)[2], float w, float 
   });
 }
 
-template <typename T, bool QK_INT8, bool CAUSAL, int D>
-__global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(pl_waves(D), pl_waves(D)))) void attn_fwd_pl_kernel(
+// SPLIT (non-causal, head_dim 64; the key-split form for grids that leave compute units idle): a
+// block of 64 queries whose two wave pairs (key groups) run the same queries on alternate 64-key
+// blocks -- group 0 the even blocks, group 1 the odd ones -- each pair with its own staging ring.
+// Each iteration both groups publish their block's row maxima in LDS before the loop's barrier
+// and read the other's after it, so both know the running max of the whole sequence up to their
+// block: block b's probabilities are shifted by exactly the max over blocks 0..b, the shift the
+// sequential loop uses, and P is bit for bit the other kernels'. Each group keeps its own row
+// sum and O^T relative to its last shift; at the end group 1 hands them to group 0 through LDS,
+// which rescales both to the larger shift and writes the output. Only the fp32 sums differ from
+// the sequential loop's (rescaled per group, then merged): rounding-level output differences.
+template <typename T, bool QK_INT8, bool CAUSAL, int D, bool SPLIT = false>
+__global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(pl_waves(D, SPLIT), pl_waves(D, SPLIT)))) void attn_fwd_pl_kernel(
     const T* __restrict__ Q, const u8* __restrict__ K8, const float* __restrict__ SKr,
     int64_t sk_plane, int64_t sk_block, const float* __restrict__ Wr, int64_t w_plane,
     int64_t w_block, float w_mul, const u8* __restrict__ V8T, const float* __restrict__ Sfold,
@@ -115,9 +127,17 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(pl_waves(D),
     int64_t o_sr, int H, int H_kv, int G, int N, int Nk, int Nk_pad, int num_qt, int xcd_span,
     float sm_scale, float* __restrict__ LSE, const float* __restrict__ KMEAN,
     const float* __restrict__ VMEAN) {
-  __shared__ PlBuf<D> sB[3];
+  static_assert(!(SPLIT && (CAUSAL || D != 64)), "the key split serves non-causal head_dim 64");
+  __shared__ PlBuf<D> sBall[SPLIT ? 6 : 3];
+  // SPLIT: the per-iteration exchange of block maxima (two slots, 4 waves x 32 queries). The
+  // block's LDS, 53248 bytes, is 26 units of 2 KB: three blocks fit a CU's 160 KB (one more
+  // 2 KB unit each would leave room for two).
+  __shared__ float xch[SPLIT ? 2 : 1][SPLIT ? 4 * 32 : 1];
   constexpr int NDT = D / 32;   // 32-channel output tiles per wave
-  constexpr int NKV = D / 64;   // 1 KB K and V^T requests per wave and block (each)
+  // 1 KB K and V^T requests per wave and block (each): a tile of D/16 KB over the 4 waves, or
+  // over the 2 waves of a key group
+  constexpr int NKV = (SPLIT ? 2 : 1) * D / 64;
+  constexpr int QB = SPLIT ? 64 : BM;          // queries per block
 
   // ---- which (plane, q-tile) this block runs: XCD-contiguous planes, longest causal tiles first
   int id = blockIdx.x;
@@ -130,26 +150,37 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(pl_waves(D),
 
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
-  const int q0 = qt * BM + w * 32;
+  // SPLIT: wave w runs query slot w & 1 of key group w >> 1 (the waves of a group: 2 of them,
+  // staging a tile together); otherwise one group of 4 waves, query slot w
+  const int kg = SPLIT ? (w >> 1) : 0;
+  const int ws = SPLIT ? (w & 1) : w;            // query slot, and staging index within the group
+  const int q0 = qt * QB + ws * 32;
   const int qrow = q0 + l32;
-
-  const u8* Kb = K8 + (int64_t)kvp * Nk_pad * D;
-  const u8* Vb = V8T + (int64_t)kvp * D * Nk_pad;
-  // wave 0 stages the SK row of each block, wave 1 the W row
-  const float* Cb = (w == 0) ? SKr + (int64_t)kvp * sk_plane : Wr + (int64_t)kvp * w_plane;
-  const uint32_t c_blk = (uint32_t)(4 * ((w == 0) ? sk_block : w_block));
+  PlBuf<D>* sB = sBall + 3 * kg;
 
   const int n_blocks = Nk_pad / BK;
-  const int j_end = CAUSAL ? min(n_blocks, (qt * BM + BM - 1) / BK + 1) : n_blocks;
+  // this group's key blocks: iteration j runs block KS * j + kg (SPLIT: kg + 2j, the even or
+  // the odd blocks), n_g of them
+  constexpr int KS = SPLIT ? 2 : 1;
+  const int n_g = SPLIT ? (n_blocks + 1 - kg) >> 1 : n_blocks;
+  const int j_end = CAUSAL ? min(n_blocks, (qt * BM + BM - 1) / BK + 1)
+                           : (SPLIT ? (n_blocks + 1) >> 1 : n_g);
   // blocks this wave computes: 0 .. w_end-1 (the rest of the j_end iterations it only stages)
-  const int w_end = CAUSAL ? min(j_end, (q0 + 31) / BK + 1) : j_end;
+  const int w_end = CAUSAL ? min(j_end, (q0 + 31) / BK + 1) : n_g;
+
+  const u8* Kb = K8 + (int64_t)kvp * Nk_pad * D + (int64_t)kg * BK * D;
+  const u8* Vb = V8T + (int64_t)kvp * D * Nk_pad + (int64_t)kg * BK;
+  // wave (slot) 0 of the group stages the SK row of each block, slot 1 the W row
+  const float* Cb = ((ws == 0) ? SKr + (int64_t)kvp * sk_plane : Wr + (int64_t)kvp * w_plane)
+                    + (int64_t)kg * ((ws == 0) ? sk_block : w_block);
+  const uint32_t c_blk = (uint32_t)(4 * KS * ((ws == 0) ? sk_block : w_block));
 
   // ---- staging: per block every wave issues NKV KB of K and NKV KB of V^T; waves 0 and 1 also
   // 256 bytes of constants (SK, W). Layouts as in attn_fwd.hip.
   uint32_t k_off[NKV], v_off[NKV];
 #pragma unroll
   for (int i = 0; i < NKV; ++i) {
-    const int I = NKV * w + i;
+    const int I = NKV * ws + i;
     const int krow = (1024 / D) * I + lane / (D / 16), kpos = lane % (D / 16);
     k_off[i] = (uint32_t)(krow * D + 16 * (kpos ^ kswz<D>(krow)));
     const int d = 16 * I + (lane >> 2), vpos = lane & 3;
@@ -157,18 +188,18 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(pl_waves(D),
   }
   const uint32_t c_off = (uint32_t)(4 * lane);
   auto dma = [&](int j, PlBuf<D>& buf) {
-    const u8* kblk = Kb + (size_t)(BK * D) * (uint32_t)j;
-    const u8* vblk = Vb + (size_t)BK * (uint32_t)j;
-    const uint32_t kl = lds_addr(buf.k) + 1024 * NKV * w, vl = lds_addr(buf.v) + 1024 * NKV * w;
+    const u8* kblk = Kb + (size_t)(KS * BK * D) * (uint32_t)j;
+    const u8* vblk = Vb + (size_t)(KS * BK) * (uint32_t)j;
+    const uint32_t kl = lds_addr(buf.k) + 1024 * NKV * ws, vl = lds_addr(buf.v) + 1024 * NKV * ws;
 #pragma unroll
     for (int i = 0; i < NKV; ++i) dma16(kblk, k_off[i], kl + 1024 * i);
 #pragma unroll
     for (int i = 0; i < NKV; ++i) dma16(vblk, v_off[i], vl + 1024 * i);
-    if (w < 2) dma4(Cb, c_off + c_blk * (uint32_t)j, lds_addr(w == 0 ? buf.c.sk : buf.c.w));
+    if (ws < 2) dma4(Cb, c_off + c_blk * (uint32_t)j, lds_addr(ws == 0 ? buf.c.sk : buf.c.w));
   };
 
-  dma(0, sB[0]);
-  if (j_end > 1) dma(1, sB[1]);
+  if (!SPLIT || n_g > 0) dma(0, sB[0]);
+  if ((SPLIT ? n_g : j_end) > 1) dma(1, sB[1]);
 
   // ---- Q: per-row quantization straight into MFMA fragments ----
   QFrag<D> qf;
@@ -188,6 +219,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(pl_waves(D),
   float m_x = -INFINITY;     // running max of x = (Q8.K8)*SK for this lane's query
   float mc = -INFINITY;      // RN(c_q * m_x), the exp2 shift in use
   float l_i = 0.0f;
+  float r_all = -INFINITY;   // SPLIT: the running max over every block both groups have run
   // P of the block whose P.V is issued next: zero before the first block and after the wave's
   // last, so that the P.V at the top of every iteration is unconditional (it adds zero there)
   i32x8 pb;
@@ -217,10 +249,16 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(pl_waves(D),
   };
 
   // The first iteration's P.V reads buffer 2's V^T tile before block 2 lands there, with P = 0:
-  // zero it, so that it adds exactly zero (uninitialized LDS may hold NaN patterns).
-  constexpr int ZB = D * BK / AT;   // bytes of the tile per thread: 16 (D = 64) or 32
+  // zero it, so that it adds exactly zero (uninitialized LDS may hold NaN patterns). A key group
+  // of the split with fewer than two blocks also reads buffers it never loads: zero those too.
+  constexpr int GT = SPLIT ? AT / 2 : AT;      // threads of a key group
+  constexpr int ZB = D * BK / GT;              // bytes of the tile per thread: 16 .. 64
+  const int gtid = SPLIT ? (tid & (GT - 1)) : tid;
+  for (int zb = SPLIT ? min(n_g, 2) : 2; zb < 3; ++zb) {
 #pragma unroll
-  for (int i = 0; i < ZB / 16; ++i) *(u32x4*)(sB[2].v + ZB * tid + 16 * i) = (u32x4){0u, 0u, 0u, 0u};
+    for (int i = 0; i < ZB / 16; ++i)
+      *(u32x4*)(sB[zb].v + ZB * gtid + 16 * i) = (u32x4){0u, 0u, 0u, 0u};
+  }
   __builtin_amdgcn_s_waitcnt(0);    // blocks 0 and 1 landed (once per block of queries)
   __syncthreads();
 
@@ -269,20 +307,56 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(pl_waves(D),
     // the softmax's first half on S^T(j): scores, masks, the running max and the block's shift
     BlockShift sh = {0.0f, 1.0f};
     float w0 = 0.0f, w1 = 0.0f;
+    float mx = -INFINITY;   // SPLIT: the row max of this group's block (-inf without one)
     if (compute) {
       w0 = kw0 * w_mul;
       w1 = kw1 * w_mul;
-      sh = scores_block<QK_INT8, CAUSAL>(st, ksk0, ksk1, j, q0, qrow, Nk, hh, cq, m_x, mc);
-      // acc *= alpha before block j's P.V (issued next iteration); P.V of block j-1 was issued
-      // above, a whole scores pass ago
-      rescale_acc(acc, sh.alpha);
+      if constexpr (SPLIT) {
+        mx = block_max<QK_INT8, false>(st, ksk0, ksk1, KS * j + kg, q0, qrow, Nk, hh);
+      } else {
+        sh = scores_block<QK_INT8, CAUSAL>(st, ksk0, ksk1, j, q0, qrow, Nk, hh, cq, m_x, mc);
+        // acc *= alpha before block j's P.V (issued next iteration); P.V of block j-1 was
+        // issued above, a whole scores pass ago
+        rescale_acc(acc, sh.alpha);
+      }
+    }
+    if constexpr (SPLIT) {
+      if (hh == 0) xch[j & 1][32 * w + l32] = mx;
     }
     // This wave's requests for block j+1 have landed; after the barrier every wave's have, and
-    // every wave has read block j-1's V^T tile, so its buffer takes block j+2.
+    // every wave has read block j-1's V^T tile, so its buffer takes block j+2. (SPLIT: and both
+    // groups' block maxima of this iteration are in LDS.)
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    if (j + 2 < j_end) dma(j + 2, bprev);
+    // SPLIT: the other group's block max (wave w ^ 2 runs the same queries), read before the
+    // staging requests are issued so that they cover its latency. The slot is written again two
+    // iterations on, after the partner has passed the next barrier.
+    float om = -INFINITY;
+    if constexpr (SPLIT) om = xch[j & 1][32 * (w ^ 2) + l32];
+    if (j + 2 < (SPLIT ? n_g : j_end)) dma(j + 2, bprev);
+    if constexpr (SPLIT) {
+      // blocks 2j (group 0) and 2j+1 (group 1) are now both known. rb: the max over blocks
+      // 0..b for this group's block b; r_all: over every block so far.
+      float rb;
+      if (kg == 0) {
+        rb = fmaxf(r_all, mx);
+        r_all = fmaxf(rb, om);
+      } else {
+        rb = fmaxf(fmaxf(r_all, om), mx);
+        r_all = rb;
+      }
+      if (compute) {
+        // scores_block's update with the sequence's max: this group's O^T and row sum are
+        // relative to the shift of its previous block (m_x, mc)
+        const float mcb = shift_of(rb, cq);
+        sh.alpha = (rb != m_x) ? __builtin_amdgcn_exp2f(mc - mcb) : 1.0f;
+        sh.mc = mcb;
+        m_x = rb;
+        mc = mcb;
+        rescale_acc(acc, sh.alpha);
+      }
+    }
     // the second half, tile by tile; S^T(j+1) tile t is issued into the registers of the scores
     // of tile t as soon as they are consumed
     if (compute) {
@@ -309,8 +383,41 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(pl_waves(D),
   for (int dt = 0; dt < NDT; ++dt) keep_live(acc[dt]);
   mfma_result_fence();
 
+  if constexpr (SPLIT) {
+    // Merge the key halves: group 1 parks O^T, mc and l of each lane in LDS (the staging ring is
+    // free once every wave has passed the barrier), group 0 takes M = max(mc0, mc1) and
+    // rescales both halves to it: l = l0 * 2^(mc0 - M) + l1 * 2^(mc1 - M), the same for O^T.
+    // A half without keys has mc = -inf, so its factor is 0.
+    constexpr int NE = 16 * NDT + 2;
+    float* park = (float*)sBall + ws * (NE * 64);
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kg == 1) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) park[(16 * dt + r) * 64 + lane] = acc[dt][r];
+      park[(16 * NDT) * 64 + lane] = mc;
+      park[(16 * NDT + 1) * 64 + lane] = l_i;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kg == 0) {
+      const float mc1 = park[(16 * NDT) * 64 + lane];
+      const float l1 = park[(16 * NDT + 1) * 64 + lane];
+      const float M = fmaxf(mc, mc1);
+      const float a0 = (mc == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mc - M);
+      const float a1 = (mc1 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mc1 - M);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          acc[dt][r] = __builtin_fmaf(acc[dt][r], a0, park[(16 * dt + r) * 64 + lane] * a1);
+      l_i = __builtin_fmaf(l_i, a0, l1 * a1);
+      mc = M;
+    }
+  }
+
   // ---------- epilogue: O = acc * S / (l * 448) (+ V's mean with smooth_v, one fma) ----------
-  if (qrow < N) {
+  if (qrow < N && kg == 0) {
     if (LSE && hh == 0) LSE[(int64_t)bh * N + qrow] = row_lse(mc, l_i, sm_scale, qmu);
     const float inv = (l_i > 0.0f) ? __fdiv_rn(Sb, l_i * P_SCALE) : 0.0f;
     T* op = O + b * o_sb + hd * o_sh + (int64_t)qrow * o_sr;
@@ -338,10 +445,10 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(pl_waves(D),
   }
 }
 
-template <typename T, bool QK_INT8, bool CAUSAL, int D>
+template <typename T, bool QK_INT8, bool CAUSAL, int D, bool SPLIT = false>
 static void launch_pl_d(const AttnArgs& a, hipStream_t stream) {
   const int BH = (int)(a.B * a.H);
-  const int num_qt = (int)((a.N + BM - 1) / BM);
+  const int num_qt = (int)((a.N + (SPLIT ? 64 : BM) - 1) / (SPLIT ? 64 : BM));
   const int total = num_qt * BH;
   const int span = (total / 8) * 8;
   // per-key constant rows: the reference's SK / SV' arrays, or the prologue's KCONST layout
@@ -349,7 +456,7 @@ static void launch_pl_d(const AttnArgs& a, hipStream_t stream) {
   const float* skr = kc ? a.kconst : a.sk;
   const float* wr = kc ? a.kconst + BK : a.svp;
   const int64_t plane = kc ? 2 * a.N_kv_pad : a.N_kv_pad, blk = kc ? 2 * BK : BK;
-  hipLaunchKernelGGL((attn_fwd_pl_kernel<T, QK_INT8, CAUSAL, D>), dim3(total), dim3(AT), 0, stream,
+  hipLaunchKernelGGL((attn_fwd_pl_kernel<T, QK_INT8, CAUSAL, D, SPLIT>), dim3(total), dim3(AT), 0, stream,
                      (const T*)a.q, (const u8*)a.k8, skr, plane, blk, wr, plane, blk,
                      kc ? 1.0f : P_SCALE, (const u8*)a.v8t, a.s, (T*)a.o, a.q_sb, a.q_sh, a.q_sr,
                      a.o_sb, a.o_sh, a.o_sr, (int)a.H, (int)a.H_kv, (int)(a.H / a.H_kv), (int)a.N,
@@ -363,6 +470,22 @@ static void launch_pl_t(const AttnArgs& a, hipStream_t stream) {
     launch_pl_d<T, QK_INT8, CAUSAL, 64>(a, stream);
   else
     launch_pl_d<T, QK_INT8, CAUSAL, 128>(a, stream);
+}
+
+template <typename T, bool QK_INT8>
+static void launch_split_t(const AttnArgs& a, hipStream_t stream) {
+  launch_pl_d<T, QK_INT8, false, 64, true>(a, stream);
+}
+
+hipError_t launch_attn_fwd_split(const AttnArgs& a, hipStream_t stream) {
+  if (a.causal || a.D != 64) return hipErrorInvalidValue;
+  if (a.dtype == 1)
+    launch_split_t<bf16, false>(a, stream);
+  else if (a.qk_int8)
+    launch_split_t<f16, true>(a, stream);
+  else
+    launch_split_t<f16, false>(a, stream);
+  return hipGetLastError();
 }
 
 hipError_t launch_attn_fwd_pl(const AttnArgs& a, hipStream_t stream) {

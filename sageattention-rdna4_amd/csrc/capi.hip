@@ -77,7 +77,9 @@ int check_grid(const char* what, int64_t blocks, int64_t threads) {
 
 // The main-loop grids: 128-query blocks of 256 threads (SAGE_KERNEL_Q128, SAGE_KERNEL_PIPE) and
 // 256-query blocks of 512 threads (SAGE_KERNEL_Q256). Checked for every kernel, so the refusal
-// does not depend on the automatic choice.
+// does not depend on the automatic choice. The key split's 64-query grid (SAGE_KERNEL_SPLIT) is
+// checked when that kernel is asked for; the automatic choice takes it only for grids of at most
+// three of its blocks per compute unit.
 int check_main_grid(int64_t B, int64_t H, int64_t N) {
   int rc = check_grid("the 128-query main loop", B * H * ((N + 127) / 128), 256);
   if (rc) return rc;
@@ -180,7 +182,14 @@ double causal_pad_work(int64_t N, int64_t tile) {
 }
 
 int kernel_for(int64_t B, int64_t H, int64_t N, int64_t D, int causal, int64_t cus) {
-  if (D != 128) return SAGE_KERNEL_PIPE;
+  if (D != 128) {
+    // head_dim 64, non-causal, when the key split's 64-query grid fits one round of three
+    // blocks per CU (its LDS bound): each wave then runs half the keys, against the pipelined
+    // kernel's one or two waves per SIMD over all of them. Beyond one round its second round
+    // runs at one wave per SIMD and the pipelined kernel is faster.
+    const int64_t nb64 = B * H * ((N + 63) / 64);
+    return (!causal && nb64 <= 3 * cus) ? SAGE_KERNEL_SPLIT : SAGE_KERNEL_PIPE;
+  }
   const int64_t nb256 = B * H * ((N + 255) / 256);
   if (causal)
     return (nb256 >= 4 * cus && causal_pad_work(N, 256) - causal_pad_work(N, 128) < 0.02)
@@ -323,6 +332,9 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
   if ((rc = check_head_dim(D))) return rc;
   if (D == 64 && kernel == SAGE_KERNEL_Q256)
     return fail(SAGE_ERR_INVALID, "kernel: the 256-query kernel serves head_dim 128 only");
+  if (kernel == SAGE_KERNEL_SPLIT && (causal || D != 64))
+    return fail(SAGE_ERR_INVALID,
+                "kernel: the key-split kernel serves non-causal head_dim 64 calls only");
   if ((rc = check_view("q", q, q_sb, q_sh, q_sr))) return rc;
   if ((rc = check_view("o", o, o_sb, o_sh, o_sr))) return rc;
   if (!k8 || !kconst || !v8t || !s) return fail(SAGE_ERR_INVALID, "an input pointer is NULL");
@@ -331,7 +343,7 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
   if (!(sm_scale > 0.0f) || !(sm_scale < 3.0e38f))
     return fail(SAGE_ERR_INVALID, "sm_scale: must be positive and finite (got %g)", (double)sm_scale);
   if (kernel != SAGE_KERNEL_AUTO && kernel != SAGE_KERNEL_Q128 && kernel != SAGE_KERNEL_Q256 &&
-      kernel != SAGE_KERNEL_PIPE)
+      kernel != SAGE_KERNEL_PIPE && kernel != SAGE_KERNEL_SPLIT)
     return fail(SAGE_ERR_INVALID, "kernel: unknown main-loop kernel code %d", kernel);
   if (lse && ((uintptr_t)lse & 3u))
     return fail(SAGE_ERR_INVALID, "ptr_align: lse must be 4-byte aligned");
@@ -374,9 +386,14 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal, const void* q, int64_t 
     if ((rc = cus_of_current_device(&cus))) return rc;
     kernel = kernel_for(B, H, N, D, causal, cus);
   }
+  if (kernel == SAGE_KERNEL_SPLIT &&
+      (rc = check_grid("the key-split main loop", B * H * ((N + 63) / 64), 256)))
+    return rc;
   hipError_t e;
   if (kernel == SAGE_KERNEL_PIPE)
     e = sage::launch_attn_fwd_pl(a, (hipStream_t)stream);
+  else if (kernel == SAGE_KERNEL_SPLIT)
+    e = sage::launch_attn_fwd_split(a, (hipStream_t)stream);
   else if (kernel == SAGE_KERNEL_Q256)
     e = sage::launch_attn_fwd_pp(a, (hipStream_t)stream);
   else

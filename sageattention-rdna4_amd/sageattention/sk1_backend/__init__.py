@@ -171,7 +171,9 @@ def sk1_forward(lib, q, k, v, *, tensor_layout="HND", is_causal=False, sm_scale=
     mean before quantizing V and adds it back to the output (exact, since each row's weights sum
     to 1; the reference's `quant_triton.py:668-678`).
     `kernel` picks the main-loop kernel (0: the library's choice by grid fill, 1: 128 queries per
-    block, 2: 256, head_dim 128 only, 3: the pipelined 128-query kernel).
+    block, 2: 256, head_dim 128 only, 3: the pipelined 128-query kernel, 4: its key split,
+    non-causal head_dim 64 only: the same probabilities as 1-3, its fp32 sums rounded in another
+    order).
     With `return_lse`, returns `(out, lse)`: lse (B, H, N) fp32, each row's natural-log
     logsumexp of its scores times sm_scale (with smooth_k, corrected by sm_scale * q . mean_k, as
     the reference's `core.py:1437-1439`).

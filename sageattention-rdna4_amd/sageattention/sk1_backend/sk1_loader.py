@@ -169,9 +169,9 @@ class SageLib:
         return int(self.lib.sage_kv_prologue_workspace_bytes(int(BH), int(N)))
 
     def kernel_choice(self, B, H, N, D, causal, cus=0):
-        """The main-loop kernel code (2: 256-query ping-pong, 3: pipelined) the library's
-        automatic choice runs for this shape on `cus` compute units (0: the current device's;
-        see `sage_attn_kernel_choice`)."""
+        """The main-loop kernel code (2: 256-query ping-pong, 3: pipelined, 4: key split) the
+        library's automatic choice runs for this shape on `cus` compute units (0: the current
+        device's; see `sage_attn_kernel_choice`)."""
         rc = int(self.lib.sage_attn_kernel_choice(int(B), int(H), int(N), int(D), int(bool(causal)),
                                                   int(cus)))
         if rc < 0:
@@ -250,8 +250,8 @@ class SageLib:
                  lse=None, kmean=None, n_kv=None, vmean=None):
         """Main loop on logical (B, H, N, D) views `q`, `o` (see `sage_attn_fwd_ex`; `kernel`:
         0 the library's choice by grid fill, 1 the 128-query kernel, 2 the 256-query ping-pong,
-        3 the pipelined 128-query kernel). The prologue outputs
-        `k8` (B*H_kv, n_pad, D) etc. give H_kv; `n_kv` is the key count (default N, and `n_pad`
+        3 the pipelined 128-query kernel, 4 its key split for non-causal head_dim 64). The
+        prologue outputs `k8` (B*H_kv, n_pad, D) etc. give H_kv; `n_kv` is the key count (default N, and `n_pad`
         is then ceil(n_kv/64)*64). `lse` (optional, (B, H, N) fp32) receives each row's
         logsumexp; `kmean` ((B*H_kv, 128) fp32) adds its smooth_k correction; `vmean`
         ((B*H_kv, 128) fp32, optional) is added to every output row (smooth_v)."""

@@ -368,16 +368,16 @@ def _cdiv(a, b):
 
 
 def _template(name):
-    """(bf16, qk_int8, causal, head_dim or None) of a main-loop kernel's mangled name."""
-    m = re.search(r"I(DF16_|DF16b)Lb([01])ELb([01])E(?:Li(\d+)E)?", name)
+    """(bf16, qk_int8, causal, head_dim, key split) of a main-loop kernel's mangled name."""
+    m = re.search(r"I(DF16_|DF16b)Lb([01])ELb([01])E(?:Li(\d+)E)?(?:Lb([01])E)?", name)
     return m.group(1) == "DF16b", m.group(2) == "1", m.group(3) == "1", \
-        int(m.group(4)) if m.group(4) else 128
+        int(m.group(4)) if m.group(4) else 128, m.group(5) == "1"
 
 
-def _attn_args(family, N, Nk, H, H_kv, D, lse=False, vmean=False):
+def _attn_args(family, N, Nk, H, H_kv, D, lse=False, vmean=False, split=False):
     """Kernel arguments in signature order, as the launchers in attn_fwd*.hip form them (B = 1,
     contiguous HND), and the number of workgroups."""
-    bm = 256 if family == "pp" else 128
+    bm = 256 if family == "pp" else 64 if split else 128
     num_qt = _cdiv(N, bm)
     total = num_qt * H
     strides = [H * N * D, N * D, D] * 2
@@ -396,7 +396,8 @@ def _attn_args(family, N, Nk, H, H_kv, D, lse=False, vmean=False):
 _CAUSAL_SHAPES = [(1, 1, 1, 1, False, False), (200, 200, 2, 1, True, False),
                   (777, 777, 1, 1, False, True)]
 _NONCAUSAL_SHAPES = [(1, 1, 1, 1, False, False), (300, 777, 4, 2, True, True),
-                     (777, 65, 1, 1, False, False), (513, 512, 1, 1, False, False)]
+                     (777, 65, 1, 1, False, False), (513, 512, 1, 1, False, False),
+                     (100, 129, 1, 1, False, False), (100, 200, 1, 1, True, False)]
 
 
 def _pick(total):
@@ -410,9 +411,9 @@ def _main_loop_cases(asm):
                else "q" if "attn_fwd_kernel" in name else None)
         if fam is None:
             continue
-        _, _, causal, D = _template(name)
+        _, _, causal, D, split = _template(name)
         for N, Nk, H, H_kv, lse, vm in (_CAUSAL_SHAPES if causal else _NONCAUSAL_SHAPES):
-            vals, total = _attn_args(fam, N, Nk, H, H_kv, D, lse, vm)
+            vals, total = _attn_args(fam, N, Nk, H, H_kv, D, lse, vm, split)
             for wg in _pick(total):
                 yield name, vals, wg, (N, Nk, H, H_kv, wg)
 
@@ -420,12 +421,15 @@ def _main_loop_cases(asm):
 @pytest.mark.parametrize("source", ["attn_fwd.hip", "attn_fwd_pp.hip", "attn_fwd_pl.hip"])
 def test_every_wave_of_a_main_loop_block_executes_the_same_barriers(source):
     asm = _assembly(os.path.join(PKG, "csrc", source))
-    seen = 0
+    seen = split = 0
     for name, vals, wg, case in _main_loop_cases(asm):
         counts, _ = asm_sim.barrier_counts(asm, name, vals, wg)
         assert len(set(counts)) == 1 and counts[0] > 0, (name, case, counts)
         seen += 1
+        split += _template(name)[4]
     assert seen >= 20
+    # the key-split forms (head_dim 64, three dtype forms), key groups of 0 to 7 blocks each
+    assert split >= (60 if source == "attn_fwd_pl.hip" else 0)
 
 
 def _prologue_geom(BH, N, N_pad, step):

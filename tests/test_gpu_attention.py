@@ -546,9 +546,108 @@ def test_d64_refuses_the_256_query_kernel():
     with pytest.raises(ValueError, match="kernel"):
         sk1_forward(SageLib.get(), q, k, v, kernel=2)
     o0 = sk1_forward(SageLib.get(), q, k, v, kernel=0)
-    o1 = sk1_forward(SageLib.get(), q, k, v, kernel=1)
+    o1 = sk1_forward(SageLib.get(), q, k, v, kernel=SageLib.get().kernel_choice(1, 2, 100, 64,
+                                                                             False))
     torch.cuda.synchronize()
     assert torch.equal(o0, o1)
+
+
+# ---------------------------------------------------------------------------------------------
+# head_dim 64 key split (kernel 4): for non-causal grids of few 128-query blocks, blocks of 64
+# queries whose two wave pairs take the even and the odd 64-key blocks and exchange their block
+# maxima every iteration, so each block's probabilities use the sequential loop's running max:
+# P is bit for bit kernel 3's, and only the fp32 row sums and O^T accumulate in another order
+# (per wave pair, merged at the end). Bars: the emulation's (cosine, rel-L1, logsumexp), and
+# against kernel 3 at most 2 units in the last place of the output dtype plus 1e-5 max|V|, the
+# logsumexp within 1e-5 (1 + |lse|). Key counts 1..4 blocks cover a wave pair with no block, one
+# block, and pairs of unequal length.
+# ---------------------------------------------------------------------------------------------
+def _split(q, k, v, **kw):
+    from sageattention.sk1_backend import sk1_forward
+    from sageattention.sk1_backend.sk1_loader import SageLib
+    r = sk1_forward(SageLib.get(), q.cuda(), k.cuda(), v.cuda(), kernel=4, **kw)
+    torch.cuda.synchronize()
+    return tuple(t.cpu() for t in r) if isinstance(r, tuple) else r.cpu()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(1, 3, 3, 1, 1), (1, 3, 3, 100, 64), (1, 3, 3, 100, 65),
+                                   (1, 3, 3, 300, 129), (1, 3, 3, 130, 192), (1, 3, 3, 65, 200),
+                                   (2, 4, 2, 777, 1000), (1, 6, 1, 64, 4999),
+                                   (1, 2, 2, 1500, 1500)],
+                         ids=lambda s: "B%dH%dkv%dN%dNk%d" % s)
+def test_d64_key_split_matches_emulation(shape, dtype):
+    B, H, H_kv, N, N_kv = shape
+    for smooth_v in (False, True):
+        q, k, v = make_qkv(B, H, N, seed=N + 3 * N_kv, dtype=dtype, k_offset_std=2.0,
+                           outlier_frac=0.01, h_kv=H_kv, n_kv=N_kv,
+                           v_offset_std=3.0 if smooth_v else 0.0, d=64)
+        print(shape, dtype, smooth_v, flush=True)
+        r = oracle.emulate_sageattn(q, k, v, is_causal=False, smooth_v=smooth_v)
+        out, lse = _split(q, k, v, return_lse=True, smooth_v=smooth_v)
+        assert torch.isfinite(out).all()
+        cs, rl = cosine(out, r["o"]), rel_l1(out, r["o"])
+        print("cos %.6f rel_l1 %.2e" % (cs, rl))
+        assert cs >= COS_MIN and rl <= REL_L1_MAX, (cs, rl)
+        _lse_close(lse, r, B, H, dtype == torch.bfloat16)
+        o3, lse3 = _forward_lse(q, k, v, smooth_v=smooth_v)
+        _close_to_kernel3(out, o3, v)
+        assert ((lse - lse3).abs() <= 1e-5 * (1 + lse3.abs())).all()
+
+
+def _close_to_kernel3(o4, o3, v):
+    ulp = 2.0 ** (-10 if o3.dtype == torch.float16 else -7)
+    err = (o4.float() - o3.float()).abs()
+    tol = 2 * ulp * o3.float().abs() + 1e-5 * v.float().abs().max().item()
+    assert (err <= tol).all(), (err.max().item(), (err - tol).max().item())
+    print("split vs kernel 3: %.3f %% of elements differ, max %.3g"
+          % (100.0 * (err > 0).float().mean().item(), err.max().item()))
+
+
+def _forward_lse(q, k, v, **kw):
+    from sageattention.sk1_backend import sk1_forward
+    from sageattention.sk1_backend.sk1_loader import SageLib
+    o, lse = sk1_forward(SageLib.get(), q.cuda(), k.cuda(), v.cuda(), kernel=3, return_lse=True,
+                         **kw)
+    torch.cuda.synchronize()
+    return o.cpu(), lse.cpu()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_d64_key_split_at_the_sdxl_shape(dtype):
+    # (1, 10, 4096, 64) non-causal (the SDXL attention shape): 320 blocks of 128 queries on 256
+    # compute units, where the automatic choice runs the key split; served call, kernel 4 and the
+    # pipelined kernel 3 all against the emulation, served == kernel 4 bit for bit, kernel 4
+    # within rounding of kernel 3
+    from sageattention.sk1_backend.sk1_loader import SageLib
+    q, k, v = make_qkv(1, 10, 4096, seed=17, dtype=dtype, k_offset_std=2.0, outlier_frac=1e-3,
+                       d=64)
+    lib = SageLib.get()
+    code = lib.kernel_choice(1, 10, 4096, 64, False)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert code == 4
+    ref = oracle.emulate_sageattn(q, k, v, is_causal=False)["o"]
+    served = _sageattn()(q.cuda(), k.cuda(), v.cuda(), is_causal=False).cpu()
+    o4 = _split(q, k, v)
+    o3 = _forward(q, k, v, causal=False, kernel=3)
+    for name, o in (("served", served), ("split", o4), ("pipelined", o3)):
+        cs, rl = cosine(o, ref), rel_l1(o, ref)
+        print(name, "cos %.6f rel_l1 %.2e" % (cs, rl))
+        assert cs >= COS_MIN and rl <= REL_L1_MAX, (name, cs, rl)
+    assert torch.equal(served, o4 if code == 4 else o3)
+    _close_to_kernel3(o4, o3, v)
+
+
+def test_key_split_refusals():
+    from sageattention.sk1_backend import sk1_forward
+    from sageattention.sk1_backend.sk1_loader import SageLib
+    lib = SageLib.get()
+    q, k, v = (t.cuda() for t in make_qkv(1, 2, 100, seed=1, d=64))
+    with pytest.raises(ValueError, match="key-split"):
+        sk1_forward(lib, q, k, v, kernel=4, is_causal=True)
+    q, k, v = (t.cuda() for t in make_qkv(1, 2, 100, seed=1, d=128))
+    with pytest.raises(ValueError, match="key-split"):
+        sk1_forward(lib, q, k, v, kernel=4)
 
 
 # ---------------------------------------------------------------------------------------------

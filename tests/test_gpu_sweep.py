@@ -4,8 +4,10 @@ Each case draws batch, heads, K/V heads (GQA/MQA), query and key lengths, head_d
 causality, smooth_k, smooth_v and return_lse, then checks:
 * `sageattn` against the CPU emulation of the reference scheme (cosine >= 0.999, rel-L1 <= 1e-2;
   the logsumexp rows within the bound of tests/test_gpu_attention.py);
-* every main-loop kernel that serves the shape (128-query, pipelined, and the 256-query ping-pong
-  at head_dim 128) bit for bit against the kernel `sageattn` chose.
+* the main-loop kernels that serve the shape with the same arithmetic (128-query, pipelined, and
+  the 256-query ping-pong at head_dim 128) bit for bit against each other, the key split
+  (non-causal head_dim 64) against the same emulation, and the call `sageattn` served bit for bit
+  against the kernel `sage_attn_kernel_choice` names.
 The draws are fixed by the case seed, so a failure names a reproducible shape.
 """
 import random
@@ -60,30 +62,42 @@ def test_random_shape(seed):
     out, lse = (res if c["lse"] else (res, None))
     out = out.cpu()
     em = oracle.emulate_sageattn(q, k, v, smooth_k=c["smooth_k"], smooth_v=c["smooth_v"], **kw)
-    assert torch.isfinite(out).all()
-    cs, rl = cosine(out, em["o"]), rel_l1(out, em["o"])
-    assert cs >= 0.999 and rl <= 1e-2, (cs, rl)
-    if c["lse"]:
-        lse = lse.cpu().double()
-        ref = em["lse"].double()
-        # the emulation's logsumexp up to 1e-3 + 1e-4 |lse|, plus the fp8 Q.K score error bound
-        # of tests/test_gpu_attention.py when Q.K is fp8 (bf16 inputs)
-        tol = 1e-3 + 1e-4 * ref.abs()
-        if c["dtype"] == torch.bfloat16:
-            sk = em["sk"].amax().item()
-            cq = em["c_q"].view_as(ref).double()
-            tol = tol + 2.0 ** -10 * 448 ** 2 * cq * sk / float(oracle.LOG2E)
-        assert ((lse - ref).abs() <= tol).all(), (lse - ref).abs().max().item()
-    # every kernel that serves the shape gives the same bits
+
+    def check(out, lse):
+        assert torch.isfinite(out).all()
+        cs, rl = cosine(out, em["o"]), rel_l1(out, em["o"])
+        assert cs >= 0.999 and rl <= 1e-2, (cs, rl)
+        if c["lse"]:
+            lse = lse.cpu().double()
+            ref = em["lse"].double()
+            # the emulation's logsumexp up to 1e-3 + 1e-4 |lse|, plus the fp8 Q.K score error
+            # bound of tests/test_gpu_attention.py when Q.K is fp8 (bf16 inputs)
+            tol = 1e-3 + 1e-4 * ref.abs()
+            if c["dtype"] == torch.bfloat16:
+                sk = em["sk"].amax().item()
+                cq = em["c_q"].view_as(ref).double()
+                tol = tol + 2.0 ** -10 * 448 ** 2 * cq * sk / float(oracle.LOG2E)
+            assert ((lse - ref).abs() <= tol).all(), (lse - ref).abs().max().item()
+
+    check(out, lse)
+    # the kernels 1-3 that serve the shape give the same bits; the key split (non-causal
+    # head_dim 64) passes the same emulation check; the served call is the chosen kernel's
     lib = SageLib.get()
-    kernels = [1, 3] + ([2] if c["D"] == 128 else [])
-    outs = []
+    kernels = [1, 3] + ([2] if c["D"] == 128 else []) + (
+        [4] if c["D"] == 64 and not c["causal"] else [])
+    outs = {}
     for kern in kernels:
         r = sk1_forward(lib, q.cuda(), k.cuda(), v.cuda(), smooth_k=c["smooth_k"],
                         smooth_v=c["smooth_v"], return_lse=c["lse"], kernel=kern, **kw)
         torch.cuda.synchronize()
-        outs.append(tuple(t.cpu() for t in r) if c["lse"] else (r.cpu(),))
-    for kern, o in zip(kernels[1:], outs[1:]):
-        for a, b in zip(outs[0], o):
+        outs[kern] = tuple(t.cpu() for t in r) if c["lse"] else (r.cpu(),)
+    for kern in kernels[1:]:
+        if kern == 4:
+            check(outs[4][0], outs[4][1] if c["lse"] else None)
+            continue
+        for a, b in zip(outs[1], outs[kern]):
             assert torch.equal(a, b), (kern, (a.float() - b.float()).abs().max().item())
-    assert torch.equal(outs[0][0], out)
+    chosen = lib.kernel_choice(c["B"], c["H"], c["N"], c["D"], c["causal"])
+    assert torch.equal(outs[chosen][0], out), chosen
+    if c["lse"]:
+        assert torch.equal(outs[chosen][1], lse.cpu()), chosen

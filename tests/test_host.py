@@ -44,6 +44,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 def test_kernel_choice_by_grid_fill():
     # The automatic main-loop choice on 256 CUs (no device query when the CU count is given).
+    # head_dim 64: the key split when not causal with at most 3 of its 64-query blocks per CU.
     # Causal: the 256-query ping-pong from 4 of its blocks per CU (1024 blocks). Non-causal: whole
     # rounds of blocks (three 128-query blocks or one 256-query block per CU) at the measured
     # per-CU throughputs 1.00 / 1.52 / 1.69 and 1.75; the ping-pong when >= 3 % sooner.
@@ -51,11 +52,18 @@ def test_kernel_choice_by_grid_fill():
     if not os.path.isfile(sk1_loader.LIB_PATH):
         pytest.skip("library not built")
     L = sk1_loader.SageLib.get()
-    Q256, PIPE = 2, 3
+    Q256, PIPE, SPLIT = 2, 3, 4
     cases = [
         # (B, H, N, D, causal, expected)
         (1, 48, 47520, 128, True, Q256),    # the headline: 8928 blocks of 256 queries
-        (1, 48, 47520, 64, True, PIPE),     # head_dim 64: always the pipelined kernel
+        (1, 48, 47520, 64, True, PIPE),     # head_dim 64 causal: always the pipelined kernel
+        (1, 10, 4096, 64, True, PIPE),
+        (1, 10, 4096, 64, False, SPLIT),    # 640 blocks of 64 queries <= 3 per CU: key split
+        (1, 12, 4096, 64, False, SPLIT),    # 768 blocks: the limit
+        (1, 13, 4096, 64, False, PIPE),     # 832 blocks
+        (1, 12, 4097, 64, False, PIPE),     # 780 blocks
+        (1, 48, 4096, 64, False, PIPE),
+        (2, 1, 1, 64, False, SPLIT),
         (1, 48, 4096, 128, True, PIPE),     # 768 blocks < 1024
         (1, 8, 32768, 128, True, Q256),     # exactly 1024 blocks
         (1, 8, 32512, 128, True, PIPE),     # 1016 blocks
@@ -121,6 +129,11 @@ def test_library_host_calls_without_a_gpu():
     # head_dim 64 or 128; 64 only on the 128-query kernel
     assert ex(D=96) == 1 and b"head_dim" in L.lib.sage_last_error()
     assert ex(D=64, kernel=2) == 1 and b"kernel" in L.lib.sage_last_error()
+    # the key split: non-causal head_dim 64 only, and its 64-query grid within HIP's limit
+    assert ex(kernel=4) == 1 and b"key-split" in L.lib.sage_last_error()
+    assert ex(D=64, causal=1, kernel=4) == 1 and b"key-split" in L.lib.sage_last_error()
+    assert ex(D=64, kernel=4, H=4194305, N=200, N_kv=100) == 1
+    assert b"the key-split main loop needs 16777220 blocks" in L.lib.sage_last_error()
     rc = L.lib.sage_quant_q(0, 1, p16, 12800, 12800, 128, 1, 1, 100, 32, ctypes.c_float(0.1),
                             p16, p16, p16, None)
     assert rc == 1 and b"head_dim" in L.lib.sage_last_error()
