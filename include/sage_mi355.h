@@ -209,8 +209,8 @@ int sage_attn_fwd_ex(int dtype, int qk_int8, int causal,
  * name the kernel.
  *   cus  compute units to plan for; <= 0: those of the current device (a device query)
  * head_dim 64 runs the key split when not causal and its grid of 64-query blocks,
- * B*H*ceil(N/64), is at most 3 per CU (one round: its LDS lets three blocks share a CU), else the
- * pipelined kernel. At 128 the 256-query ping-pong runs when, on `cus` CUs,
+ * B*H*ceil(N/64), is at most 6 per CU (two rounds: its LDS lets three blocks share a CU), else
+ * the pipelined kernel. At 128 the 256-query ping-pong runs when, on `cus` CUs,
  * its grid is estimated to finish at least 3 % sooner: a causal grid with at least 4 of its
  * blocks per CU, unless padding the last query tile to 256 rows costs over 2 % more of the causal
  * work than padding it to 128; a non-causal one by whole rounds of blocks (up to three 128-query

@@ -79,7 +79,7 @@ int check_grid(const char* what, int64_t blocks, int64_t threads) {
 // 256-query blocks of 512 threads (SAGE_KERNEL_Q256). Checked for every kernel, so the refusal
 // does not depend on the automatic choice. The key split's 64-query grid (SAGE_KERNEL_SPLIT) is
 // checked when that kernel is asked for; the automatic choice takes it only for grids of at most
-// three of its blocks per compute unit.
+// six of its blocks per compute unit.
 int check_main_grid(int64_t B, int64_t H, int64_t N) {
   int rc = check_grid("the 128-query main loop", B * H * ((N + 127) / 128), 256);
   if (rc) return rc;
@@ -183,12 +183,13 @@ double causal_pad_work(int64_t N, int64_t tile) {
 
 int kernel_for(int64_t B, int64_t H, int64_t N, int64_t D, int causal, int64_t cus) {
   if (D != 128) {
-    // head_dim 64, non-causal, when the key split's 64-query grid fits one round of three
-    // blocks per CU (its LDS bound): each wave then runs half the keys, against the pipelined
-    // kernel's one or two waves per SIMD over all of them. Beyond one round its second round
-    // runs at one wave per SIMD and the pipelined kernel is faster.
+    // head_dim 64, non-causal, with at most six of the key split's 64-query blocks per CU (two
+    // rounds of three, its LDS bound): twice the waves, each over half the keys. Measured on
+    // MI355X, 1.01-1.57x faster than the pipelined kernel there (1.24x at SDXL's 2.5 per CU);
+    // from about 8 per CU on the pipelined kernel's four resident blocks per CU catch up and
+    // from 12 on they win (0.95x at 16 and 32 per CU).
     const int64_t nb64 = B * H * ((N + 63) / 64);
-    return (!causal && nb64 <= 3 * cus) ? SAGE_KERNEL_SPLIT : SAGE_KERNEL_PIPE;
+    return (!causal && nb64 <= 6 * cus) ? SAGE_KERNEL_SPLIT : SAGE_KERNEL_PIPE;
   }
   const int64_t nb256 = B * H * ((N + 255) / 256);
   if (causal)

@@ -44,7 +44,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 def test_kernel_choice_by_grid_fill():
     # The automatic main-loop choice on 256 CUs (no device query when the CU count is given).
-    # head_dim 64: the key split when not causal with at most 3 of its 64-query blocks per CU.
+    # head_dim 64: the key split when not causal with at most 6 of its 64-query blocks per CU.
     # Causal: the 256-query ping-pong from 4 of its blocks per CU (1024 blocks). Non-causal: whole
     # rounds of blocks (three 128-query blocks or one 256-query block per CU) at the measured
     # per-CU throughputs 1.00 / 1.52 / 1.69 and 1.75; the ping-pong when >= 3 % sooner.
@@ -58,11 +58,12 @@ def test_kernel_choice_by_grid_fill():
         (1, 48, 47520, 128, True, Q256),    # the headline: 8928 blocks of 256 queries
         (1, 48, 47520, 64, True, PIPE),     # head_dim 64 causal: always the pipelined kernel
         (1, 10, 4096, 64, True, PIPE),
-        (1, 10, 4096, 64, False, SPLIT),    # 640 blocks of 64 queries <= 3 per CU: key split
-        (1, 12, 4096, 64, False, SPLIT),    # 768 blocks: the limit
-        (1, 13, 4096, 64, False, PIPE),     # 832 blocks
-        (1, 12, 4097, 64, False, PIPE),     # 780 blocks
+        (1, 10, 4096, 64, False, SPLIT),    # 640 blocks of 64 queries <= 6 per CU: key split
+        (1, 24, 4096, 64, False, SPLIT),    # 1536 blocks: the limit
+        (1, 25, 4096, 64, False, PIPE),     # 1600 blocks
+        (1, 24, 4097, 64, False, PIPE),     # 1560 blocks
         (1, 48, 4096, 64, False, PIPE),
+        (1, 30, 17550, 64, False, PIPE),    # CogVideoX-like: 32 per CU
         (2, 1, 1, 64, False, SPLIT),
         (1, 48, 4096, 128, True, PIPE),     # 768 blocks < 1024
         (1, 8, 32768, 128, True, Q256),     # exactly 1024 blocks
