@@ -33,8 +33,12 @@ __device__ __forceinline__ int kswz(int row) {
   if (D == 64) return ((row >> 2) & 1) | (((row >> 5) & 1) << 1);
   return ((row >> 1) & 1) | ((((row)&1) ^ ((row >> 2) & 1)) << 1) | (((row >> 5) & 1) << 2);
 }
-// XOR swizzle of the 16-byte chunk position within a 64-byte V^T row.
-__device__ __forceinline__ int vswz(int d) { return ((d >> 1) ^ (d >> 3)) & 3; }
+// XOR swizzle of the 16-byte chunk position within a 64-byte V^T row: bits 2-3 of the row. A P.V
+// operand read has lane l on row d = l % 32 + 32 dt, chunk 2 (l / 32) + half. Measured on gfx950
+// (8 such ds_read_b128 per wave, 4 waves per CU): 219 cycles with this swizzle or bits 3-4, as for
+// a linear read; 261 with ((d >> 1) ^ (d >> 3)) & 3, which maps rows d and d + 4 to the same two
+// chunk slots, and 512 with none. So a read pass takes lanes from both halves of the wave.
+__device__ __forceinline__ int vswz(int d) { return (d >> 2) & 3; }
 
 // Q fragments of one query row of D columns, as the S^T MFMA's B operand wants them.
 //   int8: D/32 x 16 bytes, fragment dd = columns 32dd + 16h .. +15
