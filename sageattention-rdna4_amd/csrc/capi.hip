@@ -258,7 +258,10 @@ int sage_kv_prologue(int dtype, int k_int8, int smooth_k, int smooth_v, int fold
   if (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 255u))
     return fail(SAGE_ERR_INVALID, "workspace: need %zu bytes, 256-byte aligned (got %zu)", need,
                 workspace_bytes);
+  int64_t cus = 0;
+  if ((rc = cus_of_current_device(&cus))) return rc;
   sage::PrologueArgs a;
+  a.cus = cus;
   a.dtype = dtype;
   a.k_int8 = k_int8 ? 1 : 0;
   a.smooth_k = smooth_k ? 1 : 0;
@@ -486,7 +489,10 @@ int sage_kseq_mean(int dtype, const void* k, int64_t k_sb, int64_t k_sh, int64_t
   if (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 255u))
     return fail(SAGE_ERR_INVALID, "workspace: need %zu bytes, 256-byte aligned (got %zu)", need,
                 workspace_bytes);
+  int64_t cus = 0;
+  if ((rc = cus_of_current_device(&cus))) return rc;
   sage::PrologueArgs a = {};
+  a.cus = cus;
   a.dtype = dtype;
   a.smooth_k = 1;
   a.k = k;

@@ -37,24 +37,28 @@ struct Geo {
   static constexpr int CG = D / 8, RG = PT / CG, STEP = 8 * RG, VTS = STEP + 16;
 };
 
-// Both grids are sized to one round of resident blocks on MI355X (256 CUs; a block is 4 waves, one
-// per SIMD): the stats pass fits 3 blocks per CU (at most 168 VGPRs; its 16 row loads of 16 bytes
-// per lane keep ~190 KB in flight per CU), the quant pass 8 (at most 64 VGPRs). A partly filled second round costs a streaming pass as much as a full one. Each plane gets
-// c = slots / BH blocks (at least 1) of equal row counts; a stats block's rows are a whole number
-// of its steps (128 rows for head_dim 128, 256 for 64), so no step reaches into the next block's
-// rows. A larger step only lowers C1, so the head_dim-128 geometry bounds the workspace for both.
-constexpr int64_t MI355_CUS = 256;
+// Both grids are sized to one round of resident blocks on the device's compute units (a block is 4
+// waves, one per SIMD; MI355X has 256 CUs): the stats pass fits 3 blocks per CU (at most 168
+// VGPRs; its 16 row loads of 16 bytes per lane keep ~190 KB in flight per CU), the quant pass 8
+// (at most 64 VGPRs). A partly filled second round costs a streaming pass as much as a full one.
+// Each plane gets c = slots / BH blocks (at least 1) of equal row counts; a stats block's rows are
+// a whole number of its steps (128 rows for head_dim 128, 256 for 64), so no step reaches into
+// the next block's rows. A larger step, or fewer CUs, only lowers C1, so the head_dim-128
+// geometry on MAX_CUS bounds the workspace for every call; a device with more CUs than that runs
+// the MAX_CUS grids.
+constexpr int64_t MAX_CUS = 256;
 constexpr int64_t STATS_BLOCKS_PER_CU = 3;
 constexpr int64_t QUANT_BLOCKS_PER_CU = 8;
 
-PrologueGeom prologue_geom(int64_t BH, int64_t N, int64_t N_pad, int64_t step) {
+PrologueGeom prologue_geom(int64_t BH, int64_t N, int64_t N_pad, int64_t step, int64_t cus) {
   auto cdiv = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
   auto blocks_per_plane = [&](int64_t slots) { return BH < slots ? slots / BH : (int64_t)1; };
+  const int64_t cu = (cus <= 0 || cus > MAX_CUS) ? MAX_CUS : cus;
   const int64_t Nc = cdiv(N, 64) * 64;
   PrologueGeom g;
-  g.R1 = cdiv(cdiv(Nc, blocks_per_plane(MI355_CUS * STATS_BLOCKS_PER_CU)), step) * step;
+  g.R1 = cdiv(cdiv(Nc, blocks_per_plane(cu * STATS_BLOCKS_PER_CU)), step) * step;
   g.C1 = cdiv(Nc, g.R1);
-  g.R2 = cdiv(cdiv(N_pad, blocks_per_plane(MI355_CUS * QUANT_BLOCKS_PER_CU)), 64) * 64;
+  g.R2 = cdiv(cdiv(N_pad, blocks_per_plane(cu * QUANT_BLOCKS_PER_CU)), 64) * 64;
   g.C2 = cdiv(N_pad, g.R2);
   return g;
 }
@@ -373,7 +377,7 @@ __global__ __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(QUANT_BLOCKS
 template <typename T, int D>
 static hipError_t launch_prologue_t(const PrologueArgs& a, hipStream_t stream) {
   const int64_t BH = a.B * a.H;
-  const PrologueGeom g = prologue_geom(BH, a.N, a.N_pad, Geo<D>::STEP);
+  const PrologueGeom g = prologue_geom(BH, a.N, a.N_pad, Geo<D>::STEP, a.cus);
   // region offsets as sized for head_dim 128 (prologue_workspace_bytes)
   const size_t part_bytes = part_region_bytes(BH, prologue_geom(BH, a.N, a.N_pad));
   double* part = (double*)a.workspace;
@@ -428,7 +432,7 @@ __global__ __launch_bounds__(D) void mean_reduce_kernel(const double* __restrict
 template <typename T, int D>
 static hipError_t launch_kseq_mean_t(const PrologueArgs& a, hipStream_t stream) {
   const int64_t BH = a.B * a.H;
-  const PrologueGeom g = prologue_geom(BH, a.N, a.N_pad, Geo<D>::STEP);
+  const PrologueGeom g = prologue_geom(BH, a.N, a.N_pad, Geo<D>::STEP, a.cus);
   double* part = (double*)a.workspace;
   hipLaunchKernelGGL((kv_stats_kernel<T, K_ONLY, D>), dim3((unsigned)(g.C1 * BH)), dim3(PT), 0,
                      stream, (const T*)a.k, (const T*)a.k, nullptr, nullptr, part, nullptr, nullptr,

@@ -17,7 +17,10 @@ namespace sage {
 struct PrologueGeom {
   int64_t R1, C1, R2, C2;
 };
-PrologueGeom prologue_geom(int64_t BH, int64_t N, int64_t N_pad, int64_t step = 128);
+// cus: the device's compute units; the grids are sized for min(cus, 256) (the workspace bound,
+// prologue_workspace_bytes, is the 256-CU geometry's, which has the most mean partials).
+PrologueGeom prologue_geom(int64_t BH, int64_t N, int64_t N_pad, int64_t step = 128,
+                           int64_t cus = 256);
 // bytes of workspace for BH planes of N rows (any N_pad)
 size_t prologue_workspace_bytes(int64_t BH, int64_t N);
 
@@ -38,6 +41,7 @@ struct PrologueArgs {
   float* s;
   float* kconst;   // optional: the main loop's per-key constants (B*H, N_pad/64, 2, 64) fp32
   void* workspace;
+  int64_t cus;     // compute units of the launch device (<= 0: 256)
 };
 hipError_t launch_prologue(const PrologueArgs& a, hipStream_t stream);
 // The smooth_k mean alone: K's fp64 column partials (stats pass, K only), then MEAN, with the
