@@ -638,6 +638,25 @@ def test_d64_key_split_at_the_sdxl_shape(dtype):
     _close_to_kernel3(o4, o3, v)
 
 
+def test_d64_key_split_fp8_qk_for_fp16():
+    # fp16 inputs with e4m3 Q.K (int8=False, the reference's fp8 fp16 object): the split's third
+    # instantiation, against the emulation of that form and within rounding of kernel 3
+    from sageattention.sk1_backend import sk1_forward
+    from sageattention.sk1_backend.sk1_loader import SageLib
+    q, k, v = make_qkv(2, 3, 700, seed=41, dtype=torch.float16, k_offset_std=2.0,
+                       outlier_frac=0.01, n_kv=1300, d=64)
+    ref = oracle.emulate_sageattn(q, k, v, is_causal=False, qk_int8=False)["o"]
+    outs = {}
+    for kern in (3, 4):
+        outs[kern] = sk1_forward(SageLib.get(), q.cuda(), k.cuda(), v.cuda(), int8=False,
+                                 kernel=kern).cpu()
+        torch.cuda.synchronize()
+        cs, rl = cosine(outs[kern], ref), rel_l1(outs[kern], ref)
+        print(kern, "cos %.6f rel_l1 %.2e" % (cs, rl))
+        assert cs >= COS_MIN and rl <= REL_L1_MAX, (kern, cs, rl)
+    _close_to_kernel3(outs[4], outs[3], v)
+
+
 def test_key_split_refusals():
     from sageattention.sk1_backend import sk1_forward
     from sageattention.sk1_backend.sk1_loader import SageLib
