@@ -29,6 +29,9 @@
 // Per-key constants are read from two rows per 64-key block with strides, so the same kernel reads
 // the reference's SK and SV' arrays (W = RN(SV' * 448) formed on load) or the prologue's KCONST
 // layout (W already formed, multiplied by 1).
+//
+// The SPLIT form (non-causal head_dim 64, for grids that leave compute units idle) is described
+// at the kernel: 64 queries per block, the key blocks shared out between two wave pairs.
 #include "attn_common.h"
 #include "sage_launch.h"
 

@@ -73,8 +73,8 @@ hipError_t launch_attn_fwd(const AttnArgs& a, hipStream_t stream);
 hipError_t launch_attn_fwd_pp(const AttnArgs& a, hipStream_t stream);
 // the software-pipelined form (128 queries per block of 4 waves, three or four blocks per CU)
 hipError_t launch_attn_fwd_pl(const AttnArgs& a, hipStream_t stream);
-// the same kernel in its key-split form (non-causal, head_dim 64; 64 queries per block, the two
-// halves of the keys run by two wave pairs and merged in LDS)
+// the same kernel in its key-split form (non-causal, head_dim 64; 64 queries per block, the even
+// and the odd key blocks run by two wave pairs that exchange their block maxima, merged in LDS)
 hipError_t launch_attn_fwd_split(const AttnArgs& a, hipStream_t stream);
 
 struct QuantQArgs {
