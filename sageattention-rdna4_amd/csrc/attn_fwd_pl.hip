@@ -55,62 +55,6 @@ struct __attribute__((aligned(16))) PlBuf {
 // fit a CU.
 constexpr int pl_waves(int D, bool split = false) { return split ? 3 : (D == 64 ? 4 : 3); }
 
-// S^T tile t of a 64-key block (keys 32h + 16t + reg of lane half h) for this lane's query:
-// int8 -- the bits of the int32 Q8.K8; fp8 -- the fp32 dot product.
-template <bool QK_INT8, int D>
-__device__ __forceinline__ f32x16 qk_tile(const u8* __restrict__ kbuf, const QFrag<D>& qf, int krow,
-                                          int ksw, int hh) {
-  const u8* kb = kbuf + krow * D;
-  if constexpr (QK_INT8) {
-    i32x16 a;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) a[r] = 0;
-#pragma unroll
-    for (int dd = 0; dd < D / 32; ++dd) {
-      const i32x4 kf = *(const i32x4*)(kb + 16 * ((2 * dd + hh) ^ ksw));
-      a = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf.i8[dd], a, 0, 0, 0);
-    }
-    return __builtin_bit_cast(f32x16, a);
-  } else {
-    f32x16 a;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) a[r] = 0.0f;
-#pragma unroll
-    for (int dd = 0; dd < D / 64; ++dd) {
-      const int c0 = 4 * dd + 2 * hh;
-      const i32x4 lo = *(const i32x4*)(kb + 16 * (c0 ^ ksw));
-      const i32x4 hi = *(const i32x4*)(kb + 16 * ((c0 + 1) ^ ksw));
-      const i32x8 kf = (i32x8){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-      a = mfma_f8(kf, qf.f8[dd], a);
-    }
-    return a;
-  }
-}
-
-// The exponentials, row-sum partials and e4m3 P of the 16 scores of tile T (keys 32h + 16T + r):
-// the same operations, in the same order per score and per partial sum, as probs_block
-// (attn_common.h), which does both tiles in one pass. w: the tile's W broadcast source.
-template <int T>
-__device__ __forceinline__ void probs_tile(const f32x16 (&x)[2], float w, float cq, float mc,
-                                           float (&ps)[4], i32x8& pb) {
-  // W enters through an opaque copy: otherwise its broadcasts can be hoisted away from the
-  // multiplies they fold into (one extra move, and a live register, per score)
-  asm volatile("" : "+v"(w));
-  static_for<0, 4>([&](auto k4c) {
-    constexpr int k4 = decltype(k4c)::value + 4 * T;
-    float p[4];
-    static_for<0, 4>([&](auto ec) {
-      constexpr int e = decltype(ec)::value;
-      constexpr int jj = 4 * k4 + e;
-      p[e] = __builtin_amdgcn_fmed3f(__builtin_amdgcn_exp2f(__builtin_fmaf(x[T][jj & 15], cq, -mc)),
-                                     0.0f, 1.0f);
-      ps[e] = k4 ? ps[e] + p[e] : p[e];
-      p[e] *= row_bcast<jj & 15>(w);
-    });
-    pb[k4] = (int)fp8x4(p[0], p[1], p[2], p[3]);
-  });
-}
-
 // SPLIT (non-causal, head_dim 64; the key-split form for grids that leave compute units idle): a
 // block of 64 queries whose two wave pairs (key groups) run the same queries on alternate 64-key
 // blocks -- group 0 the even blocks, group 1 the odd ones -- each pair with its own staging ring.

@@ -540,6 +540,13 @@ class Machine:
             st.scc = None if a is None or b is None else \
                 int(((a >> (b & 31)) & 1) == (1 if mn == "s_bitcmp1_b32" else 0))
             return
+        if mn in ("s_bitset0_b32", "s_bitset1_b32"):
+            # D[S0 & 31] = 0 / 1, the rest of D kept (no SCC)
+            a, b = self.sget(st, ops[0], 1), self.sget(st, ops[1], 1)
+            if a is None or b is None:
+                return self.sset(st, ops[0], None)
+            bit = 1 << (b & 31)
+            return self.sset(st, ops[0], (a | bit) if mn == "s_bitset1_b32" else (a & ~bit & M32))
         if mn in ("s_addk_i32", "s_mulk_i32"):
             a, k = self.sget(st, ops[0], 1), sx(ops[1].val & 0xFFFF, 16)
             if a is None:
