@@ -6,7 +6,9 @@ grid has 2049 query tiles per plane. Checked with properties that do not need th
   vectorized and run at this size in seconds);
 * the last 128 query rows (the longest causal rows: every key) and the first 64 equal the
   emulation's at the usual bars, computed for those rows alone (rows are independent);
-* the 128-query, pipelined and 256-query kernels agree bit for bit, and NHD equals HND.
+* the 128-query, pipelined and 256-query kernels agree bit for bit, and NHD equals HND;
+* at head_dim 64 (non-causal), the key split over 4097 key blocks (2049 and 2048 per wave pair)
+  meets the same bars on the same rows and stays within rounding of the pipelined kernel.
 """
 import pytest
 import torch
@@ -23,13 +25,13 @@ N_LONG = 262161
 def _rows_emulated(q, k, v, rows, causal):
     """The emulation's output for the query rows `rows` (a range) of plane 0."""
     kr, vr = k[0], v[0]
-    N = kr.shape[1]
+    N, D = kr.shape[1], kr.shape[2]
     n_pad = oracle.n_pad_for(N)
     mean = oracle.kseq_mean(kr)
     k8, sk = oracle.quant_k(kr, n_pad, mean=mean, int8=True)
     v8t, sv = oracle.quant_v(vr, n_pad)
     s, svp = oracle.fold_v_scale(sv)
-    q8, sq, cq = oracle.quant_q(q[0][:, rows.start:rows.stop], 128 ** -0.5, int8=True)
+    q8, sq, cq = oracle.quant_q(q[0][:, rows.start:rows.stop], D ** -0.5, int8=True)
     return oracle.attention_tiles(q8, cq, k8, sk, v8t, svp, s, N, causal, q.dtype,
                                   row0=rows.start)
 
@@ -63,3 +65,26 @@ def test_long_sequence(causal):
                          v.transpose(1, 2).contiguous().cuda(), tensor_layout="NHD", is_causal=True)
         torch.cuda.synchronize()
         assert torch.equal(o_nhd.cpu().transpose(1, 2), out)
+
+
+def test_long_sequence_head_dim_64_key_split():
+    from sageattention.sk1_backend import sk1_forward
+    from sageattention.sk1_backend.sk1_loader import SageLib
+    N = N_LONG
+    print("long N", N, "head_dim 64 key split", flush=True)
+    q, k, v = make_qkv(1, 1, N, seed=9, dtype=torch.float16, k_offset_std=2.0, outlier_frac=1e-4,
+                       d=64)
+    lib = SageLib.get()
+    outs = {}
+    for kern in (3, 4):
+        outs[kern] = sk1_forward(lib, q.cuda(), k.cuda(), v.cuda(), kernel=kern).cpu()
+        torch.cuda.synchronize()
+        assert torch.isfinite(outs[kern]).all()
+    for rows in (range(N - 128, N), range(0, 64)):
+        ref = _rows_emulated(q, k, v, rows, False)
+        for kern in (3, 4):
+            got = outs[kern][0, 0, rows.start:rows.stop]
+            c, r = cosine(got, ref[0]), rel_l1(got, ref[0])
+            assert c >= 0.999 and r <= 1e-2, (kern, rows, c, r)
+    err = (outs[4].float() - outs[3].float()).abs()
+    assert (err <= 2 * 2.0 ** -10 * outs[3].float().abs() + 1e-5 * v.float().abs().max()).all()
