@@ -574,6 +574,12 @@ def test_interpreter_follows_scalar_control_flow():
         .replace(" s_endpgm\n", " s_endpgm\n.LBB0_4:\n s_barrier\n s_endpgm\n")
     counts, _ = asm_sim.barrier_counts(skewed + meta, "_Zk", [5], 0)
     assert counts == [5, 6]
+    # s_bitset1 / s_bitset0 set and clear one bit of the destination, keeping the rest: the trip
+    # count becomes 5 | (1 << 3) = 13, then 13 & ~(1 << 0) = 12, and the final barrier makes 13
+    bits = asm.replace(" s_waitcnt lgkmcnt(0)\n", " s_waitcnt lgkmcnt(0)\n s_bitset1_b32 s4, 3\n"
+                       " s_mov_b32 s6, 0\n s_bitset0_b32 s4, s6\n")
+    counts, _ = asm_sim.barrier_counts(bits + meta, "_Zk", [5], 0)
+    assert counts == [13, 13]
 
 
 # ---------------------------------------------------------------------------------------------
