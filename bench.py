@@ -29,7 +29,9 @@ Prints ONE JSON line. Besides the contract fields it carries
   launch duration from step 4) against the int8/fp8 dense MFMA peak, and against the measured
   one (`frac_of_measured`); `traffic` is its HBM bytes per launch from the committed rocprofv3
   FETCH_SIZE/WRITE_SIZE summary for the workload (null when none is committed);
-* `prologue`: the prologue pair's achieved HBM GB/s on its algorithmic bytes;
+* `prologue`: the prologue pair's achieved HBM GB/s on its algorithmic bytes (K read twice with
+  smooth_k: once for the mean, once to quantize), and `frac_single_read`, the same time against
+  the bytes of one K read (the prologue's byte floor);
 * `cpu_baseline`: the CPU emulation of the reference scheme (`oracle/`, a "port") and torch CPU
   SDPA, timed on a bounded sample of the same workload on this host's cores;
 * `first_call`: a fresh child process's import, library load and first call of the workload's
@@ -513,6 +515,10 @@ def main():
     attn_tflops = ops / (attn_ms * 1e-3) / 1e12
     pbytes = prologue_bytes(B, H, N, D=D)
     pro_gbps = pbytes / (pro_ms * 1e-3) / 1e9
+    # the same data flow with K read once (the smooth_k mean and the quantization from one read):
+    # the byte floor of the prologue, whatever the number of passes
+    floor_bytes = prologue_bytes(B, H, N, smooth_k=False, D=D)
+    floor_gbps = floor_bytes / (pro_ms * 1e-3) / 1e9
     log("workload %s: %.3f ms/step (events %.3f), split: prologue %.3f ms (%.0f GB/s), main loop"
         " %.3f ms (%.1f TFLOP/s)" % (args.workload, ms_step, ev_ms, pro_ms, pro_gbps, attn_ms,
                                      attn_tflops))
@@ -552,7 +558,9 @@ def main():
                      "traffic": profiled_traffic(args.workload), "kernel": kname,
                      "ms": round(attn_ms, 4)},
         "prologue": {"ms": round(pro_ms, 4), "bytes": pbytes, "achieved_GBps": round(pro_gbps, 1),
-                     "peak_GBps": HBM_PEAK_GBPS, "frac": round(pro_gbps / HBM_PEAK_GBPS, 4)},
+                     "peak_GBps": HBM_PEAK_GBPS, "frac": round(pro_gbps / HBM_PEAK_GBPS, 4),
+                     "single_read_bytes": floor_bytes,
+                     "frac_single_read": round(floor_gbps / HBM_PEAK_GBPS, 4)},
         "cpu_baseline": cpu,
         "first_call": first,
         # the timed region's HIP-event time per call, the split pass's per-call times, and the
