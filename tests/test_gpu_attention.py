@@ -1,7 +1,9 @@
 """The gfx950 main loop and the `sageattn` drop-in against the oracle and exact attention (GPU).
 
 Bars (north star): cosine >= 0.999 and relative L1 <= 1e-2 against the CPU emulation of the
-reference scheme; error against exact attention reported and held to the reference's own bar,
+reference scheme, the relative L1 tightened to this build's regression bar of the Q.K form
+(`sage_testutil.REL_L1_REGRESSION`); error against exact attention reported and held to the
+reference's own bar,
 relative RMS < 0.08 against fp32 SDPA (`tests/test_sk1_backend.py:28-29` of the reference).
 The reference's behaviour tests are mirrored: edge lengths, a |V| = 20000 outlier, NHD == HND
 bitwise, int8 as the fp16 default, fused-QKV views bitwise.
@@ -11,13 +13,12 @@ import torch
 import torch.nn.functional as F
 
 import oracle
-from sage_testutil import (HEAD_DIM, cosine, have_gfx950, make_qkv, rel_l1, rel_rms)
+from sage_testutil import (COS_MIN, HEAD_DIM, cosine, have_gfx950, make_qkv, rel_l1,
+                            rel_l1_bar, rel_rms)
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not have_gfx950(), reason="needs a gfx950 GPU")]
 
-COS_MIN = 0.999
-REL_L1_MAX = 1e-2
 MAX_REL_RMS = 0.08
 
 
@@ -77,7 +78,8 @@ def _check_vs_oracle(q, k, v, *, causal, smooth_k=True, layout="HND", sm_scale=N
     assert torch.isfinite(out).all()
     cs, rl = cosine(out, ref), rel_l1(out, ref)
     print("cos %.6f rel_l1 %.2e" % (cs, rl))
-    assert cs >= COS_MIN and rl <= REL_L1_MAX, (cs, rl)
+    int8_qk = q.dtype == torch.float16 and int8 is not False
+    assert cs >= COS_MIN and rl <= rel_l1_bar(int8_qk), (cs, rl)
     return out, ref
 
 
@@ -242,7 +244,7 @@ def test_q256_kernel_matches_emulation(causal, dtype):
     ref = oracle.emulate_sageattn(q, k, v, tensor_layout="HND", is_causal=causal)["o"]
     out = _forward(q, k, v, causal=causal, kernel=2)
     assert cosine(out, ref) >= COS_MIN
-    assert rel_l1(out, ref) <= REL_L1_MAX
+    assert rel_l1(out, ref) <= rel_l1_bar(dtype == torch.float16)
 
 
 def test_q256_kernel_nhd_equals_hnd_bitwise():
@@ -296,7 +298,8 @@ def test_return_lse_matches_emulation(N, dtype, causal, smooth_k, layout):
     lse = lse.cpu()
     assert torch.isfinite(lse).all()
     err = _lse_close(lse, r, B, H, dtype == torch.bfloat16)
-    assert cosine(out.cpu(), r["o"]) >= COS_MIN and rel_l1(out.cpu(), r["o"]) <= REL_L1_MAX
+    assert cosine(out.cpu(), r["o"]) >= COS_MIN
+    assert rel_l1(out.cpu(), r["o"]) <= rel_l1_bar(dtype == torch.float16)
     ex = oracle.exact_lse(q, k, is_causal=causal, tensor_layout=layout).float()
     qerr = (lse - ex).abs()
     print("lse: vs emulation %.2e, vs exact %.3e (mean %.3e)"
@@ -358,7 +361,7 @@ def test_gqa_and_kv_length_match_emulation(shape, dtype):
         assert out.shape == q.shape and lse.shape == (B, H, N)
         cs, rl = cosine(out, r["o"]), rel_l1(out, r["o"])
         print("cos %.6f rel_l1 %.2e" % (cs, rl))
-        assert cs >= COS_MIN and rl <= REL_L1_MAX, (cs, rl)
+        assert cs >= COS_MIN and rl <= rel_l1_bar(dtype == torch.float16), (cs, rl)
         _lse_close(lse, r, B, H, dtype == torch.bfloat16)
         if not outliers:
             assert rel_rms(out, oracle.exact_attention(q, k, v, is_causal=causal)) < MAX_REL_RMS
@@ -421,7 +424,7 @@ def test_smooth_v_matches_emulation(N, dtype, causal, layout):
                       smooth_v=True).cpu()
     cs, rl = cosine(out, r["o"]), rel_l1(out, r["o"])
     print("cos %.6f rel_l1 %.2e" % (cs, rl))
-    assert cs >= COS_MIN and rl <= REL_L1_MAX, (cs, rl)
+    assert cs >= COS_MIN and rl <= rel_l1_bar(dtype == torch.float16), (cs, rl)
     if N > 1:
         ex = oracle.exact_attention(q, k, v, is_causal=causal, tensor_layout=layout)
         plain = _sageattn()(q.cuda(), k.cuda(), v.cuda(), tensor_layout=layout,
@@ -445,7 +448,7 @@ def test_smooth_v_against_the_reference_fp32_mean(N, dtype, causal):
     out = _sageattn()(q.cuda(), k.cuda(), v.cuda(), is_causal=causal, smooth_v=True).cpu()
     cs, rl = cosine(out, r["o"]), rel_l1(out, r["o"])
     print("cos %.6f rel_l1 %.2e" % (cs, rl))
-    assert cs >= COS_MIN and rl <= REL_L1_MAX, (cs, rl)
+    assert cs >= COS_MIN and rl <= rel_l1_bar(dtype == torch.float16), (cs, rl)
     vr = v.reshape(3, N, 128)
     ref32 = oracle.vseq_mean_fp32_chunked(vr).double()
     ours = oracle.kseq_mean(vr).double()      # the prologue's VMEAN bits (bit-exact elsewhere)
@@ -535,7 +538,7 @@ def test_d64_gqa_lse_smooth_v_match_emulation(shape, dtype):
         out, lse = out.cpu(), lse.cpu()
         cs, rl = cosine(out, r["o"]), rel_l1(out, r["o"])
         print(shape, dtype, smooth_v, "cos %.6f rel_l1 %.2e" % (cs, rl))
-        assert cs >= COS_MIN and rl <= REL_L1_MAX, (cs, rl)
+        assert cs >= COS_MIN and rl <= rel_l1_bar(dtype == torch.float16), (cs, rl)
         _lse_close(lse, r, B, H, dtype == torch.bfloat16)
 
 
@@ -588,7 +591,7 @@ def test_d64_key_split_matches_emulation(shape, dtype):
         assert torch.isfinite(out).all()
         cs, rl = cosine(out, r["o"]), rel_l1(out, r["o"])
         print("cos %.6f rel_l1 %.2e" % (cs, rl))
-        assert cs >= COS_MIN and rl <= REL_L1_MAX, (cs, rl)
+        assert cs >= COS_MIN and rl <= rel_l1_bar(dtype == torch.float16), (cs, rl)
         _lse_close(lse, r, B, H, dtype == torch.bfloat16)
         o3, lse3 = _forward_lse(q, k, v, smooth_v=smooth_v)
         _close_to_kernel3(out, o3, v)
@@ -633,7 +636,7 @@ def test_d64_key_split_at_the_sdxl_shape(dtype):
     for name, o in (("served", served), ("split", o4), ("pipelined", o3)):
         cs, rl = cosine(o, ref), rel_l1(o, ref)
         print(name, "cos %.6f rel_l1 %.2e" % (cs, rl))
-        assert cs >= COS_MIN and rl <= REL_L1_MAX, (name, cs, rl)
+        assert cs >= COS_MIN and rl <= rel_l1_bar(dtype == torch.float16), (name, cs, rl)
     assert torch.equal(served, o4 if code == 4 else o3)
     _close_to_kernel3(o4, o3, v)
 
@@ -653,7 +656,7 @@ def test_d64_key_split_fp8_qk_for_fp16():
         torch.cuda.synchronize()
         cs, rl = cosine(outs[kern], ref), rel_l1(outs[kern], ref)
         print(kern, "cos %.6f rel_l1 %.2e" % (cs, rl))
-        assert cs >= COS_MIN and rl <= REL_L1_MAX, (kern, cs, rl)
+        assert cs >= COS_MIN and rl <= rel_l1_bar(False), (kern, cs, rl)
     _close_to_kernel3(outs[4], outs[3], v)
 
 

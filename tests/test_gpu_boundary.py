@@ -13,7 +13,8 @@ import pytest
 import torch
 
 import oracle
-from sage_testutil import bytes_equal, cosine, have_gfx950, make_qkv, mismatch_report, rel_l1
+from sage_testutil import (bytes_equal, cosine, have_gfx950, make_qkv, mismatch_report, rel_l1,
+                           rel_l1_bar)
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not have_gfx950(), reason="needs a gfx950 GPU")]
@@ -94,7 +95,7 @@ def test_main_loop_on_sk_svp_matches_emulation():
                        ref["svp"].cuda(), ref["s"].cuda(), o, qk_int8=True, causal=True,
                        sm_scale=128 ** -0.5)
     torch.cuda.synchronize()
-    assert cosine(o.cpu(), em) >= 0.999 and rel_l1(o.cpu(), em) <= 1e-2
+    assert cosine(o.cpu(), em) >= 0.999 and rel_l1(o.cpu(), em) <= rel_l1_bar(True)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -153,7 +154,7 @@ def test_more_planes_than_a_grid_dimension():
                          is_causal=causal).cpu()
         assert torch.equal(out[:, pick], alone)
         em = oracle.emulate_sageattn(qs, ks, vs, tensor_layout="HND", is_causal=causal)["o"]
-        assert cosine(alone, em) >= 0.999 and rel_l1(alone, em) <= 1e-2
+        assert cosine(alone, em) >= 0.999 and rel_l1(alone, em) <= rel_l1_bar(True)
         assert torch.isfinite(out).all()
 
 

@@ -18,7 +18,8 @@ import pytest
 import torch
 
 import oracle
-from sage_testutil import cosine, have_gfx950, make_qkv, quantized_bit_exact, rel_l1
+from sage_testutil import (cosine, have_gfx950, make_qkv, quantized_bit_exact, rel_l1,
+                           rel_l1_bar)
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not have_gfx950(), reason="needs a gfx950 GPU")]
@@ -43,7 +44,7 @@ def test_benchmark_length_parity(name, dtype, B, H, N, causal, layout, k_off, ou
     out = out.cpu()
     assert out.shape == q.shape and torch.isfinite(out).all()
     c, r = cosine(out, emu), rel_l1(out, emu)
-    assert c >= 0.999 and r <= 1e-2, (c, r)
+    assert c >= 0.999 and r <= rel_l1_bar(dtype == torch.float16), (c, r)
     from sageattention.sk1_backend import sk1_forward
     from sageattention.sk1_backend.sk1_loader import SageLib
     lib = SageLib.get()

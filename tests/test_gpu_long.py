@@ -14,7 +14,8 @@ import pytest
 import torch
 
 import oracle
-from sage_testutil import cosine, have_gfx950, make_qkv, quantized_bit_exact, rel_l1
+from sage_testutil import (cosine, have_gfx950, make_qkv, quantized_bit_exact, rel_l1,
+                           rel_l1_bar)
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not have_gfx950(), reason="needs a gfx950 GPU")]
@@ -54,7 +55,7 @@ def test_long_sequence(causal):
         ref = _rows_emulated(q, k, v, rows, causal)
         got = out[0, 0, rows.start:rows.stop]
         c, r = cosine(got, ref[0]), rel_l1(got, ref[0])
-        assert c >= 0.999 and r <= 1e-2, (rows, c, r)
+        assert c >= 0.999 and r <= rel_l1_bar(True), (rows, c, r)
     lib = SageLib.get()
     for kern in (1, 2, 3):
         o = sk1_forward(lib, q.cuda(), k.cuda(), v.cuda(), is_causal=causal, kernel=kern)
@@ -85,6 +86,6 @@ def test_long_sequence_head_dim_64_key_split():
         for kern in (3, 4):
             got = outs[kern][0, 0, rows.start:rows.stop]
             c, r = cosine(got, ref[0]), rel_l1(got, ref[0])
-            assert c >= 0.999 and r <= 1e-2, (kern, rows, c, r)
+            assert c >= 0.999 and r <= rel_l1_bar(True), (kern, rows, c, r)
     err = (outs[4].float() - outs[3].float()).abs()
     assert (err <= 2 * 2.0 ** -10 * outs[3].float().abs() + 1e-5 * v.float().abs().max()).all()

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import oracle
-from sage_testutil import cosine, have_gfx950, make_qkv, rel_l1
+from sage_testutil import cosine, have_gfx950, make_qkv, rel_l1, rel_l1_bar
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not have_gfx950(), reason="needs a gfx950 GPU")]
@@ -48,7 +48,7 @@ def test_pipelined_matches_emulation(causal, dtype):
     q, k, v = make_qkv(2, 2, 1337, seed=11, dtype=dtype, k_offset_std=2.0, outlier_frac=0.001)
     ref = oracle.emulate_sageattn(q, k, v, tensor_layout="HND", is_causal=causal)["o"]
     out = _run(q, k, v, causal=causal, kernel=PIPE)
-    assert cosine(out, ref) >= 0.999 and rel_l1(out, ref) <= 1e-2
+    assert cosine(out, ref) >= 0.999 and rel_l1(out, ref) <= rel_l1_bar(dtype == torch.float16)
 
 
 GQA_SHAPES = [

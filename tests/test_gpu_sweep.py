@@ -16,7 +16,7 @@ import pytest
 import torch
 
 import oracle
-from sage_testutil import cosine, have_gfx950, make_qkv, rel_l1
+from sage_testutil import cosine, have_gfx950, make_qkv, rel_l1, rel_l1_bar
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not have_gfx950(), reason="needs a gfx950 GPU")]
@@ -66,7 +66,7 @@ def test_random_shape(seed):
     def check(out, lse):
         assert torch.isfinite(out).all()
         cs, rl = cosine(out, em["o"]), rel_l1(out, em["o"])
-        assert cs >= 0.999 and rl <= 1e-2, (cs, rl)
+        assert cs >= 0.999 and rl <= rel_l1_bar(c["dtype"] == torch.float16), (cs, rl)
         if c["lse"]:
             lse = lse.cpu().double()
             ref = em["lse"].double()

@@ -17,7 +17,7 @@ import pytest
 import torch
 
 import oracle
-from sage_testutil import cosine, emulate_rows, have_gfx950, make_qkv, rel_l1
+from sage_testutil import cosine, emulate_rows, have_gfx950, make_qkv, rel_l1, rel_l1_bar
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not have_gfx950(), reason="needs a gfx950 GPU")]
@@ -76,7 +76,7 @@ def test_large_shape(seed):
             ref_lse.append(lse_r)
     got, ref = torch.cat(got, dim=2), torch.cat(ref, dim=2)
     cs, rl = cosine(got, ref), rel_l1(got, ref)
-    assert cs >= 0.999 and rl <= 1e-2, (cs, rl)
+    assert cs >= 0.999 and rl <= rel_l1_bar(c["dtype"] == torch.float16), (cs, rl)
     if c["lse"]:
         g = torch.cat(got_lse, dim=2).double()
         e = torch.cat(ref_lse, dim=2).double()
@@ -114,4 +114,4 @@ def test_large_shape(seed):
             o_hnd = oracle.to_hnd(o, c["layout"])
             g = torch.cat([o_hnd[:, :, rows.start:rows.stop] for rows in slices], dim=2)
             cs, rl = cosine(g, ref), rel_l1(g, ref)
-            assert cs >= 0.999 and rl <= 1e-2, (kern, cs, rl)
+            assert cs >= 0.999 and rl <= rel_l1_bar(c["dtype"] == torch.float16), (kern, cs, rl)

@@ -414,6 +414,22 @@ def test_planted_mistakes_are_caught(name, monkeypatch):
     assert mismatched_rows(_mutated_attention_tiles(old, new)) > 0, name
 
 
+def test_fp16_rounded_probabilities_fail_the_regression_bar(monkeypatch):
+    # The GPU tests hold outputs to the north star's rel-L1 <= 1e-2 tightened to the regression
+    # bar of their Q.K form (sage_testutil.REL_L1_REGRESSION). A per-score chain that rounds p at
+    # fp16 level, planted here into a copy of the oracle's loop, stays inside 1e-2 but not inside
+    # the int8 bar: about 1 % of its e4m3 P codes cross a rounding boundary.
+    import oracle.sage_scheme as mod
+    from sage_testutil import REL_L1_MAX, rel_l1, rel_l1_bar
+    q, k, v = make_qkv(1, 2, 1024, seed=3, k_offset_std=2.0)
+    ref = mod.emulate_sageattn(q, k, v)["o"]
+    monkeypatch.setattr(mod, "attention_tiles", _mutated_attention_tiles(
+        "p = torch.exp2(s - m_use[:, :, None])",
+        "p = torch.exp2(s - m_use[:, :, None]).half().float()"))
+    rl = rel_l1(mod.emulate_sageattn(q, k, v)["o"], ref)
+    assert rel_l1_bar(True) < rl < REL_L1_MAX, rl
+
+
 def test_nhd_layout_is_a_view():
     q, k, v = make_qkv(2, 3, 100, seed=1)
     a = oracle.emulate_sageattn(q, k, v, is_causal=True)["o"]
