@@ -213,8 +213,8 @@ def test_other_head_dims_are_refused(d):
 
 
 # ---------------------------------------------------------------------------------------------
-# The two main-loop kernels (128 queries per block, and 256 per block in two ping-pong groups)
-# compute every query with the same instructions in the same order, so they must agree bitwise;
+# The 128- and 256-query main-loop kernels (128 queries per block, and 256 per block in two
+# ping-pong groups; the pipelined kernel has tests of its own) compute every query with the same instructions in the same order, so they must agree bitwise;
 # the 256-query kernel is also held to the oracle directly, at lengths that exercise its tile
 # edges (256-row tiles, causal diagonals inside a tile, ragged tails) and its staging depth.
 # ---------------------------------------------------------------------------------------------
