@@ -3,10 +3,10 @@
 Bars (north star): cosine >= 0.999 and relative L1 <= 1e-2 against the CPU emulation of the
 reference scheme, the relative L1 tightened to this build's regression bar of the Q.K form
 (`sage_testutil.REL_L1_REGRESSION`); error against exact attention reported and held to the
-reference's own bar,
-relative RMS < 0.08 against fp32 SDPA (`tests/test_sk1_backend.py:28-29` of the reference).
-The reference's behaviour tests are mirrored: edge lengths, a |V| = 20000 outlier, NHD == HND
-bitwise, int8 as the fp16 default, fused-QKV views bitwise.
+reference's own bar, relative RMS < 0.08 against fp32 SDPA (`tests/test_sk1_backend.py:28-29` of
+the reference). The reference's behaviour tests are mirrored: edge lengths, a |V| = 20000
+outlier, NHD == HND bitwise, int8 as the fp16 default, fused-QKV views bitwise; and its offline
+gate of magnitude sweeps.
 """
 import pytest
 import torch
@@ -164,6 +164,61 @@ def test_large_v_outlier_stays_finite(dtype):
     assert torch.isfinite(out).all()
     ref = oracle.emulate_sageattn(q, k, v)["o"]
     assert cosine(out, ref) >= COS_MIN
+
+
+# Magnitude sweep (the reference's offline gate of outlier sweeps past 448, `docs/METHOD.md:47-78`):
+# Q, K and V each scaled by 1e-3 (fp16 subnormals), 1, 30 or 500 (|x| in the thousands, V's fold
+# S > 1; 1 % of the keys x8, which keeps fp16 K finite), 64 combinations per dtype, causal on every
+# other one. Every quantized tensor's scales follow the magnitudes, so the output must stay within
+# the bars of its Q.K form.
+_SCALES = (1e-3, 1.0, 30.0, 500.0)
+_MAGNITUDES = [(a, b, c) for a in _SCALES for b in _SCALES for c in _SCALES]
+
+
+def _reorderable_rows(r, N, causal):
+    """e4m3 Q.K, H_kv == H: (BH, N) rows whose two largest scores (log2 units, from the
+    emulation's exact sums) lie within twice the MFMA's score error bound of each other, the
+    bound of `_lse_close` over the row's real keys, 2^-10 * 448^2 * c_q * max SK. The hardware's
+    sums are not exactly rounded, so it may put either key first."""
+    sk = r["sk"][:, :N].double()
+    s = torch.matmul(r["q8"].double(), r["k8"][:, :N].double().transpose(1, 2))
+    s = s * r["c_q"].double()[:, :, None] * sk[:, None, :]
+    if causal:
+        s = s.masked_fill(torch.ones(N, N, dtype=torch.bool).triu(1)[None], -float("inf"))
+    if N < 2:
+        return torch.zeros(s.shape[:2], dtype=torch.bool)
+    top = s.topk(2, dim=2).values
+    eps = 2.0 ** -10 * 448.0 ** 2 * r["c_q"].double() * sk.amax(dim=1)[:, None]
+    return (top[..., 0] - top[..., 1]) < 2 * eps
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("mags", _MAGNITUDES, ids=lambda m: "q%g-k%g-v%g" % m)
+def test_magnitude_sweep_matches_emulation(mags, dtype):
+    # int8 Q.K sums exactly: the output is held to the bars. e4m3 Q.K: the bars hold over every
+    # row except those that differ from the emulation by more than 1e-2 (rel-L1) while their two
+    # best keys are within the MFMA's score error of each other. At Q and K x500 the logits
+    # reach ~1e7 log2 units, and two keys 3e-7 apart (relative) then swap.
+    sq_, sk_, sv_ = mags
+    causal = _MAGNITUDES.index(mags) % 2 == 1
+    N = 257
+    q, k, v = make_qkv(1, 2, N, seed=_MAGNITUDES.index(mags), dtype=torch.float32,
+                       k_offset_std=2.0, outlier_frac=0.01, outlier_scale=8.0)
+    q, k, v = ((t * s).to(dtype) for t, s in ((q, sq_), (k, sk_), (v, sv_)))
+    print("scales", mags, dtype, "causal", causal, flush=True)
+    if dtype == torch.float16:
+        _check_vs_oracle(q, k, v, causal=causal)
+        return
+    r = oracle.emulate_sageattn(q, k, v, is_causal=causal)
+    out = _sageattn()(q.cuda(), k.cuda(), v.cuda(), is_causal=causal).cpu()
+    assert torch.isfinite(out).all()
+    o, e = out.reshape(2, N, -1).double(), r["o"].reshape(2, N, -1).double()
+    row_err = (o - e).abs().sum(-1) / e.abs().sum(-1).clamp_min(1e-30)
+    swapped = (row_err > 1e-2) & _reorderable_rows(r, N, causal)
+    assert swapped.sum() <= 2, int(swapped.sum())
+    cs, rl = cosine(o[~swapped], e[~swapped]), rel_l1(o[~swapped], e[~swapped])
+    print("cos %.6f rel_l1 %.2e, %d rows swapped" % (cs, rl, int(swapped.sum())))
+    assert cs >= COS_MIN and rl <= rel_l1_bar(False), (cs, rl)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
