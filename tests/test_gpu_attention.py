@@ -131,6 +131,16 @@ def test_config4_bf16_causal():
     _check_vs_oracle(q, k, v, causal=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("sm_scale", [1e-3, 0.05, 0.3, 1.0, 4.0])
+def test_sm_scale_matches_emulation(sm_scale, causal, dtype):
+    # sm_scale other than 1/sqrt(D) enters c_q (Q's scale times sm_scale times log2 e): from an
+    # almost uniform softmax (1e-3) to a sharply peaked one (4.0)
+    q, k, v = make_qkv(1, 2, 300, seed=int(sm_scale * 1000) + 1, dtype=dtype, k_offset_std=2.0)
+    _check_vs_oracle(q, k, v, causal=causal, sm_scale=sm_scale)
+
+
 @pytest.mark.parametrize("N", [288, 512])
 def test_config5_short_calls(N):
     q, k, v = make_qkv(1, 48, N, seed=N, dtype=torch.float16)
